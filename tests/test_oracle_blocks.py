@@ -1,0 +1,145 @@
+"""Pins the oracle's RMSNorm, attention and SwiGLU pieces.
+
+Each check compares against something the mathematics fixes independently of
+the oracle's code: closed forms, brute force in float64 with Python loops on
+tiny shapes, and special cases (pos = 0, identical keys, a dominant score,
+GQA as MHA with repeated heads). The bf16 rounding points of the "mk" mode are
+checked on a hand-computed case (attention.py:354-392: exp cast to bf16 before
+PV, fp32 denominator).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle.llama_ref import Dims, OracleLlama
+
+
+def bare(mode="exact", d=None):
+    o = OracleLlama.__new__(OracleLlama)
+    o.mode = mode
+    o.dt = torch.float64 if mode == "exact" else torch.float32
+    o.d = d or Dims(hidden=8, n_q=4, n_kv=1, head_dim=4)
+    o.scale = 1.0 / math.sqrt(o.d.head_dim)
+    return o
+
+
+def test_rmsnorm_closed_forms():
+    o = bare(d=Dims(hidden=2048))
+    for c in (0.5, -3.0, 1e-3):
+        x = torch.full((2048,), c, dtype=torch.float64)
+        y = o.norm_scale(x)
+        expect = math.copysign(1.0, c) / math.sqrt(1 + 1e-5 / (c * c))
+        assert torch.allclose(y, torch.full_like(y, expect), rtol=1e-12)
+    z = o.norm_scale(torch.zeros(2048, dtype=torch.float64))
+    assert torch.all(z == 0)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2048, dtype=torch.float64, generator=g)
+    ms = sum(float(v) ** 2 for v in x) / 2048
+    ref = x / math.sqrt(ms + 1e-5)
+    assert torch.allclose(o.norm_scale(x), ref, rtol=1e-12, atol=1e-14)
+
+
+def brute_attention(q, K, V, n_valid, scale):
+    """float64 loops: q [T, n_q, D], K/V [n_kv, S, D]; head h reads kv h // (n_q/n_kv)."""
+    T, n_q, D = q.shape
+    n_kv = K.shape[0]
+    g = n_q // n_kv
+    out = torch.zeros(T, n_q, D, dtype=torch.float64)
+    for t in range(T):
+        for h in range(n_q):
+            kv = h // g
+            s = [scale * sum(float(q[t, h, e]) * float(K[kv, j, e]) for e in range(D))
+                 for j in range(n_valid[t])]
+            m = max(s)
+            p = [math.exp(x - m) for x in s]
+            den = sum(p)
+            for e in range(D):
+                out[t, h, e] = sum(p[j] * float(V[kv, j, e]) for j in range(n_valid[t])) / den
+    return out
+
+
+def test_attention_matches_bruteforce():
+    d = Dims(hidden=16, n_q=4, n_kv=2, head_dim=4)
+    o = bare(d=d)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(3, 4, 4, dtype=torch.float64, generator=g)
+    K = torch.randn(2, 7, 4, dtype=torch.float64, generator=g)
+    V = torch.randn(2, 7, 4, dtype=torch.float64, generator=g)
+    n_valid = [3, 5, 7]
+    got = o.attention(q, K, V, torch.tensor(n_valid))
+    ref = brute_attention(q, K, V, n_valid, 0.5)
+    assert torch.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_special_cases():
+    d = Dims(hidden=16, n_q=4, n_kv=1, head_dim=4)
+    o = bare(d=d)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, 4, 4, dtype=torch.float64, generator=g)
+    K = torch.randn(1, 6, 4, dtype=torch.float64, generator=g)
+    V = torch.randn(1, 6, 4, dtype=torch.float64, generator=g)
+    # pos = 0: only the fresh row -> output is that V row exactly
+    out = o.attention(q, K, V, torch.tensor([1]))
+    assert torch.equal(out[0], V[0, 0].expand(4, 4))
+    # identical keys -> uniform average of V
+    K2 = K[:, :1].expand(1, 6, 4).clone()
+    out = o.attention(q, K2, V, torch.tensor([6]))
+    assert torch.allclose(out[0], V[0].mean(0).expand(4, 4), rtol=1e-12)
+    # one dominant score -> one-hot
+    K3 = K.clone()
+    K3[0, 4] = q[0, 0] * 1e4
+    out = o.attention(q[:, :1].expand(1, 4, 4), K3, V, torch.tensor([6]))
+    assert torch.allclose(out[0, 0], V[0, 4], atol=1e-9)
+    # masked rows never contribute, even if they hold inf / nan
+    K4, V4 = K.clone(), V.clone()
+    K4[0, 3:] = float("inf")
+    V4[0, 3:] = float("nan")
+    a = o.attention(q, K4, V4, torch.tensor([3]))
+    b = o.attention(q, K[:, :3], V[:, :3], torch.tensor([3]))
+    assert torch.equal(a, b)
+
+
+def test_gqa_equals_mha_with_repeated_heads():
+    d_gqa = Dims(hidden=16, n_q=4, n_kv=2, head_dim=4)
+    d_mha = Dims(hidden=16, n_q=4, n_kv=4, head_dim=4)
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(2, 4, 4, dtype=torch.float64, generator=g)
+    K = torch.randn(2, 5, 4, dtype=torch.float64, generator=g)
+    V = torch.randn(2, 5, 4, dtype=torch.float64, generator=g)
+    a = bare(d=d_gqa).attention(q, K, V, torch.tensor([4, 5]))
+    b = bare(d=d_mha).attention(q, K.repeat_interleave(2, 0), V.repeat_interleave(2, 0),
+                                 torch.tensor([4, 5]))
+    assert torch.equal(a, b)
+    # and the grouping is h -> h // 2 (not h % 2): swapping kv heads changes head 0
+    c = bare(d=d_gqa).attention(q, K.flip(0), V.flip(0), torch.tensor([4, 5]))
+    assert not torch.allclose(a[:, 0], c[:, 0])
+
+
+def test_mk_attention_rounding_points():
+    """exp cast to bf16 in the numerator only; denominator from fp32 exp."""
+    d = Dims(hidden=4, n_q=1, n_kv=1, head_dim=4)
+    o = bare("mk", d)
+    q = torch.tensor([[[1.0, 0.5, -0.25, 0.125]]])
+    K = torch.tensor([[[0.3, -0.7, 0.2, 0.9], [1.1, 0.4, -0.6, 0.05], [-0.2, 0.8, 0.33, -0.41]]])
+    V = torch.tensor([[[1.0, 2.0, 3.0, 4.0], [-1.5, 0.25, 2.5, -3.0], [0.7, -0.9, 1.3, 0.1]]])
+    s = [0.5 * sum(q[0, 0, e].item() * K[0, j, e].item() for e in range(4)) for j in range(3)]
+    s32 = torch.tensor(s, dtype=torch.float32)
+    p = torch.exp(s32 - s32.max())
+    pb = p.to(torch.bfloat16).float()
+    num = (pb[:, None] * V[0]).sum(0)
+    expect = (num * (1.0 / p.sum())).to(torch.bfloat16).float()
+    got = o.attention(q, K, V, torch.tensor([3]))[0, 0]
+    assert torch.allclose(got, expect, atol=0, rtol=0) or (got - expect).abs().max() <= 2 ** -8 * expect.abs().max()
+    # the bf16 rounding of p is visible: differs from the unrounded result
+    exact = ((p[:, None] * V[0]).sum(0) / p.sum())
+    assert not torch.equal(num, (p[:, None] * V[0]).sum(0))
+    assert (got - exact).abs().max() < 1e-2
+
+
+def test_swiglu_closed_form():
+    x = torch.linspace(-6, 6, 101, dtype=torch.float64)
+    u = torch.linspace(2, -1, 101, dtype=torch.float64)
+    ref = x / (1 + torch.exp(-x)) * u
+    assert torch.allclose(torch.nn.functional.silu(x) * u, ref, rtol=1e-13, atol=1e-15)
