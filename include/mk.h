@@ -1,0 +1,166 @@
+/*
+ * mk.h — C ABI of libmk.so, the MI355X (gfx950) Llama-3.2-1B decode megakernel.
+ *
+ * One call runs one token-generation step of all requested decoder layers in a
+ * single persistent kernel launch, optionally followed by the final RMSNorm,
+ * the tied lm_head GEMV and a greedy argmax, on the caller's HIP stream.
+ *
+ * Every pointer in mk_weights / mk_step_args is a device pointer owned by the
+ * caller (PyTorch tensors in this repository), except k_cache / v_cache, which
+ * are host arrays holding one device pointer per layer. The library never
+ * allocates, frees or synchronises inside mk_decode_step.
+ *
+ * Reference interfaces this ABI replaces (keaganchern/llama1B-megakernel):
+ *   - transformer_llama_megakernel_16layers(X, Wq_all, Wk_all, Wv_all, Wo_all,
+ *       gpre_all, Wgu_all, Wd_all, gpost_all, K_00..K_15, V_00..V_15, cos, sin,
+ *       position_ids) -> (Y, K_00..K_15, V_00..V_15)
+ *       transformer_llama.py:196-241 (body 90-144)       -> mk_decode_step
+ *   - transformer_llama_megakernel_1layer(...)  transformer_llama.py:154-191
+ *                                                          -> mk_layer_step
+ *   - the lm_head / sampling of NxDI's token-generation graph
+ *       (llama.py:1208-1227, main.py:57, 291)              -> mk_decode_step
+ *         with logits / next_token set
+ *
+ * Error convention: 0 on success, a negative MK_ERR_* code otherwise, with a
+ * message from mk_last_error(). Arguments are validated before any HIP call.
+ * Faults the device detects while running (a position out of range, a grid
+ * barrier that timed out) set bits in the workspace; mk_read_device_error()
+ * returns and clears them.
+ */
+#ifndef MK_H_
+#define MK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK_ABI_VERSION 1
+
+#define MK_OK                0
+#define MK_ERR_NULL         -1   /* a required pointer is NULL                  */
+#define MK_ERR_SHAPE        -2   /* layer count, batch, s_max, rope_rows        */
+#define MK_ERR_WORKSPACE    -3   /* workspace too small or misaligned           */
+#define MK_ERR_UNSUPPORTED  -4   /* a valid request this build does not run     */
+#define MK_ERR_HIP          -5   /* a HIP runtime call failed                   */
+#define MK_ERR_DEVICE       -6   /* device cannot co-schedule the persistent grid */
+#define MK_ERR_ALIGN        -7   /* a pointer is not 16-byte aligned            */
+
+/* Device-side error bits (mk_read_device_error). */
+#define MK_DEVERR_POS        0x1u  /* pos[b] < 0 or >= s_max or >= rope_rows: step skipped */
+#define MK_DEVERR_BARRIER    0x2u  /* a grid barrier exceeded its time limit */
+
+/* mk_step_args.flags */
+#define MK_FLAG_ADVANCE      0x1u  /* after the step: pos[b] += 1 (device side)   */
+
+/* Model constants the kernel is built for (Llama-3.2-1B). */
+#define MK_HIDDEN      2048
+#define MK_N_Q_HEADS   32
+#define MK_N_KV_HEADS  8
+#define MK_HEAD_DIM    64
+#define MK_INTER       8192
+#define MK_VOCAB       128256
+#define MK_MAX_LAYERS  16
+#define MK_QKV_ROWS    3072
+
+/*
+ * Packed, layer-stacked weights (all bf16, row-major [out][in]).
+ * Counterpart of the eight mk_*_stack parameters built by
+ * NeuronLlamaForCausalLMMK.convert_hf_to_neuron_state_dict
+ * (llama_with_megakernel.py:281-351), in this build's own layout:
+ *   w_qkv     [L][3072][2048]  Q,K,V rows in RoPE pairs (d, d+32) of a head:
+ *                              Q heads, then K heads, then V heads; the
+ *                              input_layernorm gamma folded in.
+ *   w_o       [L][2048][2048]  o_proj.weight
+ *   w_gu      [L][16384][2048] rows (gate_i, up_i) interleaved; the
+ *                              post_attention_layernorm gamma folded in.
+ *   w_down    [L][2048][8192]  down_proj.weight
+ *   embed     [128256][2048]   token embedding, also the tied lm_head
+ *   norm_final[2048]           final RMSNorm gamma
+ *   rope      [rope_rows][128] bf16 cos(64) | sin(64) per position
+ *                              (replaces the per-step cos/sin kernel inputs)
+ */
+typedef struct mk_weights {
+    const void *w_qkv;
+    const void *w_o;
+    const void *w_gu;
+    const void *w_down;
+    const void *embed;
+    const void *norm_final;
+    const void *rope;
+    int32_t n_layers;    /* layers present in the stacks (1..16)       */
+    int32_t rope_rows;   /* rows of the rope table (>= s_max)          */
+} mk_weights;
+
+/*
+ * One decode step.
+ *   layers [first_layer, first_layer + n_layers) run, in order.
+ *   Input: tokens[b] (embedding gather) or hidden_in[b][2048] (bf16);
+ *          exactly one of the two is non-NULL.
+ *   k_cache[i], v_cache[i]: layer first_layer+i, bf16 [batch][8][s_max][64].
+ *          The fresh K (after RoPE) and V rows are written in place at row
+ *          pos[b]; attention reads rows [0, pos[b]] (the fresh row included).
+ *          Nothing else in the caches is read or written.
+ *   pos[b]: device int32, 0 <= pos[b] < s_max.
+ *   hidden_out: bf16 [batch][2048] hidden state after the last layer (before
+ *          the final norm), or NULL.
+ *   logits: fp32 [batch][128256] or NULL; next_token: int32 [batch] greedy
+ *          argmax (lowest index on ties) or NULL. If both are NULL the final
+ *          norm and lm_head are skipped (the layer-stack seam of
+ *          transformer_llama.py). next_token may alias tokens.
+ *   workspace: device memory of at least mk_workspace_bytes(batch, s_max)
+ *          bytes, 256-byte aligned, zeroed once with mk_workspace_init before
+ *          first use; every step leaves it ready for the next.
+ *   stream: hipStream_t (NULL = default stream).
+ * Calls on one workspace must not overlap in time (same stream, or ordered).
+ */
+typedef struct mk_step_args {
+    int32_t first_layer;
+    int32_t n_layers;
+    int32_t batch;
+    int32_t s_max;
+    void *const *k_cache;
+    void *const *v_cache;
+    const int32_t *tokens;
+    const void *hidden_in;
+    int32_t *pos;
+    void *hidden_out;
+    float *logits;
+    int32_t *next_token;
+    uint32_t flags;
+    void *workspace;
+    size_t workspace_bytes;
+    void *stream;
+} mk_step_args;
+
+/* Library / device information. */
+int mk_abi_version(void);
+const char *mk_last_error(void);
+/* Grid size (workgroups, one per CU) the kernel uses on `device`; <0 on error. */
+int mk_grid_size(int device);
+
+/* Workspace bytes for `batch` sequences with `s_max` cache rows; 0 if unsupported. */
+size_t mk_workspace_bytes(int32_t batch, int32_t s_max);
+/* Zero the workspace on `stream` with a fill kernel (graph-capturable). */
+int mk_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+/* Synchronise `stream`, return the device error bits and clear them. */
+int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);
+
+/* The decode step (see mk_step_args). Asynchronous on the stream. */
+int mk_decode_step(const mk_weights *w, const mk_step_args *a);
+
+/*
+ * Single-layer step (transformer_llama_megakernel_1layer,
+ * transformer_llama.py:154-191): layer `layer` of the stacks applied to
+ * hidden_in, result in hidden_out, K/V row pos[b] written in place.
+ */
+int mk_layer_step(const mk_weights *w, int32_t layer, int32_t batch, int32_t s_max,
+                  void *k_cache, void *v_cache, const void *hidden_in, int32_t *pos,
+                  void *hidden_out, void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MK_H_ */

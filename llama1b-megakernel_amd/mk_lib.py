@@ -1,0 +1,157 @@
+"""ctypes binding of ``libmk.so`` (declared in ``include/mk.h``) and a small
+device-state holder used by the Python seams.
+
+This is the only module that talks to the native library. The library must be
+built (``build_lib.py``); if it is missing, ``load()`` raises — there is no
+fallback implementation of the decode step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_int, c_int32, c_size_t, c_uint32, c_void_p
+from pathlib import Path
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmk.so")
+
+MK_OK = 0
+ERRORS = {
+    -1: "MK_ERR_NULL", -2: "MK_ERR_SHAPE", -3: "MK_ERR_WORKSPACE", -4: "MK_ERR_UNSUPPORTED",
+    -5: "MK_ERR_HIP", -6: "MK_ERR_DEVICE", -7: "MK_ERR_ALIGN",
+}
+MK_DEVERR_POS = 0x1
+MK_DEVERR_BARRIER = 0x2
+MK_FLAG_ADVANCE = 0x1
+
+HIDDEN, N_KV, HEAD_DIM, VOCAB, MAX_LAYERS = 2048, 8, 64, 128256, 16
+
+
+class MkWeights(ctypes.Structure):
+    _fields_ = [
+        ("w_qkv", c_void_p), ("w_o", c_void_p), ("w_gu", c_void_p), ("w_down", c_void_p),
+        ("embed", c_void_p), ("norm_final", c_void_p), ("rope", c_void_p),
+        ("n_layers", c_int32), ("rope_rows", c_int32),
+    ]
+
+
+class MkStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("first_layer", c_int32), ("n_layers", c_int32), ("batch", c_int32), ("s_max", c_int32),
+        ("k_cache", POINTER(c_void_p)), ("v_cache", POINTER(c_void_p)),
+        ("tokens", c_void_p), ("hidden_in", c_void_p), ("pos", c_void_p),
+        ("hidden_out", c_void_p), ("logits", c_void_p), ("next_token", c_void_p),
+        ("flags", c_uint32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("stream", c_void_p),
+    ]
+
+
+class MkError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libmk.so (raises FileNotFoundError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(f"{LIB_PATH} is missing: build it with build_lib.py")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.mk_abi_version.restype = c_int
+        lib.mk_last_error.restype = c_char_p
+        lib.mk_grid_size.argtypes = [c_int]
+        lib.mk_grid_size.restype = c_int
+        lib.mk_workspace_bytes.argtypes = [c_int32, c_int32]
+        lib.mk_workspace_bytes.restype = c_size_t
+        lib.mk_workspace_init.argtypes = [c_void_p, c_size_t, c_void_p]
+        lib.mk_workspace_init.restype = c_int
+        lib.mk_read_device_error.argtypes = [c_void_p, c_void_p, POINTER(c_uint32)]
+        lib.mk_read_device_error.restype = c_int
+        lib.mk_decode_step.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
+        lib.mk_decode_step.restype = c_int
+        lib.mk_layer_step.argtypes = [POINTER(MkWeights), c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                      c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.mk_layer_step.restype = c_int
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != MK_OK:
+        raise MkError(rc, load().mk_last_error().decode(errors="replace"))
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def current_stream_ptr() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def weights_struct(packed: Dict[str, torch.Tensor]) -> MkWeights:
+    """MkWeights view of ``mk_weights.pack_for_megakernel`` output (device tensors)."""
+    for k in ("w_qkv", "w_o", "w_gu", "w_down", "embed", "norm_final", "rope"):
+        t = packed[k]
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError(f"{k} must be contiguous bf16")
+    return MkWeights(
+        _ptr(packed["w_qkv"]), _ptr(packed["w_o"]), _ptr(packed["w_gu"]), _ptr(packed["w_down"]),
+        _ptr(packed["embed"]), _ptr(packed["norm_final"]), _ptr(packed["rope"]),
+        int(packed["w_qkv"].shape[0]), int(packed["rope"].shape[0]))
+
+
+class Workspace:
+    """Device workspace for one stream of steps (zeroed once at creation)."""
+
+    def __init__(self, batch: int, s_max: int, device: torch.device):
+        lib = load()
+        n = lib.mk_workspace_bytes(batch, s_max)
+        if n == 0:
+            raise MkError(-4, f"no workspace size for batch={batch}, s_max={s_max}")
+        self.nbytes = (n + 255) // 256 * 256
+        # torch's caching allocator returns 512-byte aligned blocks
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
+        assert self.buf.data_ptr() % 256 == 0
+        check(lib.mk_workspace_init(self.buf.data_ptr(), self.nbytes, c_void_p(current_stream_ptr())))
+
+    def read_device_error(self) -> int:
+        bits = c_uint32(0)
+        check(load().mk_read_device_error(self.buf.data_ptr(), c_void_p(current_stream_ptr()),
+                                          ctypes.byref(bits)))
+        return bits.value
+
+
+def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tensor],
+                v_caches: Sequence[torch.Tensor], pos: torch.Tensor, *,
+                tokens: Optional[torch.Tensor] = None, hidden_in: Optional[torch.Tensor] = None,
+                hidden_out: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None,
+                next_token: Optional[torch.Tensor] = None, first_layer: int = 0,
+                n_layers: Optional[int] = None, flags: int = 0, batch: int = 1) -> None:
+    """One call of ``mk_decode_step`` on the current torch stream."""
+    n = len(k_caches) if n_layers is None else n_layers
+    if len(k_caches) < n or len(v_caches) < n:
+        raise ValueError("need one K and one V cache per layer run")
+    s_max = int(k_caches[0].shape[-2])
+    kc = (c_void_p * n)(*[t.data_ptr() for t in k_caches[:n]])
+    vc = (c_void_p * n)(*[t.data_ptr() for t in v_caches[:n]])
+    a = MkStepArgs(first_layer, n, batch, s_max, ctypes.cast(kc, POINTER(c_void_p)),
+                   ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
+                   _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes,
+                   current_stream_ptr())
+    check(load().mk_decode_step(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def header_functions(header: Path) -> List[str]:
+    """Names of the functions declared in include/mk.h."""
+    import re
+    text = header.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mk_\w+)\s*\(", text, flags=re.M)
