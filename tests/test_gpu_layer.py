@@ -5,8 +5,11 @@ bf16 ~ N(0,1), pos = 1023 (and a few other positions), run through
 ``mk_layer_step`` / ``mk_decode_step`` in libmk.so and compared with
 ``OracleLlama`` in "mk" mode (same bf16 rounding points, fp32 accumulation):
 
-* output hidden within 2 bf16 ulps elementwise (summation order differs, so a
-  value may round to the neighbouring bf16);
+* output hidden within 2^-6 * max(|ref|, 1) elementwise (a few bf16 ulps:
+  summation order differs, so intermediates may round to the neighbouring
+  bf16, and the kernel's split-K softmax keeps p in fp32), and the rms of the
+  GPU-oracle difference no larger than 1.5x the rms by which the bf16 oracle
+  itself departs from float64 math ("exact" mode) on the same inputs;
 * the K/V scatter is position-exact: every cache byte outside row ``pos`` of
   each kv head is unchanged, and the written rows match the oracle's
   RoPE'd K and V within 1 bf16 ulp (almost all bit-exact);
@@ -48,11 +51,12 @@ def run_layer(packed, hidden, kc, vc, pos_val, ws=None):
     return out, ws
 
 
-def oracle_layer(sd, d, hidden_cpu, k0, v0, pos_val):
+def oracle_layer(sd, d, hidden_cpu, k0, v0, pos_val, mode="mk"):
     from oracle.llama_ref import OracleLlama
-    o = OracleLlama(sd, d, mode="mk")
-    cache = [(k0[0].float().clone(), v0[0].float().clone())]
-    _, h = o.forward(None, pos_val, cache, hidden=hidden_cpu.float(), want_logits=False)
+    o = OracleLlama(sd, d, mode=mode)
+    dt = o.dt
+    cache = [(k0[0].to(dt).clone(), v0[0].to(dt).clone())]
+    _, h = o.forward(None, pos_val, cache, hidden=hidden_cpu.to(dt), want_logits=False)
     return h, cache
 
 
@@ -72,8 +76,12 @@ def test_layer_matches_oracle(layer_setup, pos_val):
     ulp = bf16_ulp(ref)
     say(f"[layer] pos={pos_val} max|d|={diff.max().item():.3e} max ulps={(diff / ulp).max().item():.2f} "
         f"frac!=0: {(diff > 0).float().mean().item():.4f}")
-    assert torch.all(diff <= 2 * ulp + 1e-6)
-    assert (diff > ulp).float().mean().item() < 0.01
+    assert torch.all(diff <= 2.0 ** -6 * ref.abs().clamp_min(1.0))
+    exact, _ = oracle_layer(sd, d, hidden, k0, v0, pos_val, mode="exact")
+    rms_gpu = (got.double() - ref.double()).pow(2).mean().sqrt().item()
+    rms_bf16 = (ref.double() - exact).pow(2).mean().sqrt().item()
+    say(f"[layer] pos={pos_val} rms(gpu-mk)={rms_gpu:.3e} rms(mk-exact)={rms_bf16:.3e}")
+    assert rms_gpu <= 1.5 * rms_bf16 + 1e-6
 
     # scatter: only row pos changed, in every kv head
     k1, v1 = kc[0].cpu(), vc[0].cpu()
