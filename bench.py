@@ -1,0 +1,173 @@
+#!/usr/bin/env python3
+"""Benchmark: bs=1 Llama-3.2-1B decode on one MI355X (BASELINE.json metric).
+
+Workload ("C3"): random-init bf16 weights (seed 0),
+a 384-token uniform-random prompt prefilled into a 1024-row KV cache by the
+megakernel itself, then greedy decode. A *step* is one decode step — one
+launch of the persistent megakernel (16 layers + final norm + tied lm_head +
+argmax) for one token; the token and position are fed back on the device, so
+consecutive steps need no host work. W untimed warm-up steps run first, the
+state is rewound, and exactly K steps are timed from position 384 (K <= 640,
+so the timed steps cover KV lengths 384..384+K-1).
+
+Printed (one JSON line on stdout): tok/s over the timed region (host clock,
+synchronised on both sides), ms per step, p50/p90 step latency from HIP events
+on the kernel's stream, the HBM roofline of the megakernel (algorithmic bytes
+per step / mean step time vs 8 TB/s), and a CPU baseline: the oracle's fp32
+decode step timed on this host's cores on a bounded sample.
+
+``--gpus N`` with N > 1 exits: this benchmark runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "llama1b-megakernel_amd"))
+sys.path.insert(1, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+PROMPT = 384
+S_MAX = 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(sd, n_steps: int, budget_s: float):
+    """The oracle's decode step (fp32 accumulation, bf16 rounding points) on the
+    host cores, at positions 384.. with a synthetic N(0,1) KV cache."""
+    import torch
+    from oracle.llama_ref import OracleLlama
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    o = OracleLlama(sd, mode="mk")
+    g = torch.Generator().manual_seed(1)
+    cache = [(torch.randn(8, S_MAX, 64, generator=g).to(torch.bfloat16).float(),
+              torch.randn(8, S_MAX, 64, generator=g).to(torch.bfloat16).float()) for _ in range(16)]
+    log(f"[cpu] oracle ready in {time.perf_counter() - t0:.1f}s, {threads} threads")
+    tok = torch.tensor([17])
+    o.forward(tok, PROMPT, cache)              # warm-up step
+    times = []
+    t_start = time.perf_counter()
+    for i in range(n_steps):
+        t = time.perf_counter()
+        logits, _ = o.forward(tok, PROMPT + 1 + i, cache)
+        tok = logits.argmax(-1)
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    total = sum(times)
+    return {
+        "value": round(len(times) / total, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": f"{len(times)} oracle decode steps (fp32 accumulation, bf16 rounding points) at positions "
+                  f"{PROMPT + 1}..{PROMPT + len(times)} with a synthetic N(0,1) bf16 KV cache; "
+                  f"p50 {statistics.median(times) * 1e3:.1f} ms/step",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=640)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-steps", type=int, default=24)
+    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        sys.exit(2)
+    if not 1 <= args.steps <= S_MAX - PROMPT:
+        sys.exit(f"--steps must be in [1, {S_MAX - PROMPT}]")
+
+    import torch
+    import mk_lib
+    from mk_config import step_bytes
+    from llama_with_megakernel import NeuronLlamaForCausalLM, NeuronConfigLlamaMK, LlamaInferenceConfig
+    from mk_weights import random_token_ids
+
+    t0 = time.perf_counter()
+    cfg = LlamaInferenceConfig(NeuronConfigLlamaMK(seq_len=S_MAX, max_context_length=S_MAX))
+    model = NeuronLlamaForCausalLM("random:0", cfg)
+    model.compile()
+    model.load()
+    log(f"[bench] weights packed in {time.perf_counter() - t0:.1f}s; grid = {mk_lib.load().mk_grid_size(0)} WGs")
+
+    prompt = random_token_ids(PROMPT, seed=0)
+    model.prefill(prompt)
+    dec = model.launcher("decode")
+    dec.launch()                                 # position 383 -> first generated token
+    torch.cuda.synchronize()
+    pos0 = model.pos.clone()
+    tok0 = model.tokens.clone()
+    assert int(pos0.item()) == PROMPT
+
+    for _ in range(args.warmup):
+        dec.launch()
+    torch.cuda.synchronize()
+    model.pos.copy_(pos0)
+    model.tokens.copy_(tok0)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    evs[0].record()
+    for i in range(K):
+        dec.launch()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    bits = model.ws.read_device_error()
+    if bits:
+        sys.exit(f"device error bits 0x{bits:x}")
+    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
+    mean_ms = sum(step_ms) / K
+    bytes_per_step = sum(step_bytes(16, [PROMPT + i], lm_head=True) for i in range(K)) / K
+    achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "bs=1 decode tok/s + p50 step latency, Llama-3.2-1B ctx1024; HBM GB/s",
+        "value": round(K / wall, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "p50_step_ms": round(statistics.median(step_ms), 4),
+        "p90_step_ms": round(sorted(step_ms)[int(0.9 * (K - 1))], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights seed 0, uniform-random prompt ids seed 0)",
+        "config": {"workload": "C3: Llama-3.2-1B decode, batch 1, 384-token prompt prefilled to a 1024-row "
+                               f"KV cache, greedy steps at KV lengths {PROMPT}..{PROMPT + K - 1}",
+                   "batch": 1, "prompt": PROMPT, "max_context_length": S_MAX, "n_layers": 16},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_step": int(bytes_per_step), "kernel": "mk_decode_kernel"},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del model
+        torch.cuda.empty_cache()
+        from mk_weights import synthetic_state_dict
+        sd = synthetic_state_dict(seed=0)
+        result["cpu_baseline"] = cpu_baseline(sd, args.cpu_steps, args.cpu_budget_s)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -133,13 +133,22 @@ typedef struct mk_step_args {
     void *workspace;
     size_t workspace_bytes;
     void *stream;
+    /* Optional phase trace (NULL = off): device uint64 [grid][MK_TRACE_SLOTS].
+     * Workgroup w records the device wall clock (mk_wall_clock_hz ticks/s) in
+     * slot 0 at start, 2k-1 when it arrives at grid barrier k (k = 1, 2, ...),
+     * 2k when its wait on barrier k returns, and MK_TRACE_SLOTS-1 at exit. */
+    void *trace;
 } mk_step_args;
+
+#define MK_TRACE_SLOTS 256
 
 /* Library / device information. */
 int mk_abi_version(void);
 const char *mk_last_error(void);
 /* Grid size (workgroups, one per CU) the kernel uses on `device`; <0 on error. */
 int mk_grid_size(int device);
+/* Frequency of the device wall clock used by the trace (ticks per second). */
+long long mk_wall_clock_hz(int device);
 
 /* Workspace bytes for `batch` sequences with `s_max` cache rows; 0 if unsupported. */
 size_t mk_workspace_bytes(int32_t batch, int32_t s_max);

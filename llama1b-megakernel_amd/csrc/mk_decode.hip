@@ -18,8 +18,15 @@
 //     launched cooperatively so all workgroups are co-resident;
 //   * phases are separated by a grid barrier built from device-scope atomics:
 //     each barrier has its own NCTR arrival counters on separate 128-byte
-//     lines (one release add per workgroup), wave 0 of each workgroup polls
-//     them, every wave then issues an agent-scope acquire;
+//     lines (one relaxed add per workgroup), wave 0 of each workgroup polls
+//     them. There is no L2 writeback or invalidate at a barrier (an
+//     agent-scope release/acquire costs ~10 us per phase on 8 XCDs): data a
+//     workgroup hands to others is written with device-scope (sc1) stores,
+//     each wave waits for its stores to complete (s_waitcnt vmcnt(0)) before
+//     its workgroup arrives, every activation buffer is written once per launch
+//     (one set per layer) so no XCD's L2 can hold a stale copy and readers
+//     keep the L2 hits, and the one buffer rewritten within a launch (the
+//     split-K partials) is read with device-scope loads;
 //   * weights stream once from HBM through bounds-checked buffer loads
 //     (16 B per lane, fully coalesced 1 KiB per wave per load); rows past a
 //     wave's share are out-of-range offsets that return zero without a memory
@@ -81,12 +88,12 @@ constexpr size_t BAR_BYTES = (size_t)MAX_BARRIERS * NCTR * CTR_STRIDE * 4;
 constexpr size_t OFF_MISC = BAR_BYTES;                 // exit counter, error bits, head counters, argmax key
 constexpr size_t MISC_EXIT = 0, MISC_ERR = 1, MISC_HEAD = 16;   // u32 indices
 constexpr size_t MISC_KEY_BYTE = 128;                           // u64
-constexpr size_t OFF_HA = OFF_MISC + 256;
-constexpr size_t OFF_HB = OFF_HA + H * 2;
-constexpr size_t OFF_Q = OFF_HB + H * 2;
-constexpr size_t OFF_ATT = OFF_Q + H * 2;
-constexpr size_t OFF_ACT = OFF_ATT + H * 2;
-constexpr size_t OFF_PART = OFF_ACT + INTER * 2;
+// Activation buffers, one set per layer (each written once per launch):
+//   h1 [2048] | q [2048] | att [2048] | act [8192] | h2 [2048]   (bf16)
+constexpr size_t ACT_H1 = 0, ACT_Q = H * 2, ACT_ATT = 2 * H * 2, ACT_ACT = 3 * H * 2,
+                 ACT_H2 = 3 * H * 2 + INTER * 2, ACT_LAYER_BYTES = 4 * H * 2 + INTER * 2;
+constexpr size_t OFF_ACTS = OFF_MISC + 256;
+constexpr size_t OFF_PART = OFF_ACTS + (size_t)MK_MAX_LAYERS * ACT_LAYER_BYTES;
 
 inline int max_split_for(int s_max) { return (s_max + ATT_ROWS - 1) / ATT_ROWS; }
 inline size_t ws_bytes_for(int s_max) {
@@ -138,13 +145,33 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+constexpr int AUX_NT = 2, AUX_SC1 = 16;   // buffer-load cache policy bits (gfx950)
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 // Streaming 16-byte load (non-temporal); offsets >= the resource size read zero.
 __device__ __forceinline__ u32x4 ld_stream(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_NT);
 }
+
+// Device-scope (sc1) accesses for data exchanged between workgroups within a
+// launch: the store writes through to the device coherence point, the load
+// never returns a line cached before that point was updated.
+__device__ __forceinline__ void st_dev(uint16_t* p, uint32_t bf_bits) {
+  __hip_atomic_store(p, (uint16_t)bf_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u32x4 ld_dev16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_SC1);
+}
+// Completion of this wave's outstanding memory operations (stores included).
+__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
@@ -183,6 +210,7 @@ struct KParams {
   uint32_t flags;
   int max_split;
   unsigned long long timeout_ticks;
+  unsigned long long* trace;
 };
 
 // ---------------------------------------------------------------------------
@@ -195,44 +223,55 @@ struct Grid {
   int wg;
   int k;                       // number of arrivals issued so far
   unsigned long long timeout;
+  unsigned long long* trace;   // this workgroup's MK_TRACE_SLOTS slots, or null
 };
 
+__device__ __forceinline__ void trace_mark(const Grid& g, int slot) {
+  if (g.trace && threadIdx.x == 0 && slot < MK_TRACE_SLOTS) g.trace[slot] = wall_clock64();
+}
+
+// Arrive: every wave's stores are complete, then one relaxed add per workgroup.
 __device__ __forceinline__ void grid_arrive(Grid& g) {
+  wait_mem();
   __syncthreads();
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(g.bar + ((size_t)g.k * NCTR + (g.wg % NCTR)) * CTR_STRIDE, 1u,
-                           __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ++g.k;
+  trace_mark(g, 2 * g.k - 1);
 }
 
-// Wait until every workgroup has arrived at barrier k (scalar arguments so the
-// caller's state stays in registers).
-__device__ __noinline__ void grid_wait_k(uint32_t* bar, uint32_t* err, int G, int k,
-                                         unsigned long long timeout) {
+// Wait until every workgroup has arrived at barrier `k` (0-based). Wave 0
+// polls; the other waves wait at the workgroup barrier without draining their
+// in-flight weight loads.
+__device__ __forceinline__ void grid_wait_k(const Grid& g, int k) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const int c = lane < NCTR ? lane : 0;
-    const uint32_t need = lane < NCTR ? (uint32_t)(G / NCTR + (lane < G % NCTR ? 1 : 0)) : 0u;
-    uint32_t* a = bar + ((size_t)k * NCTR + c) * CTR_STRIDE;
+    const uint32_t need = lane < NCTR ? (uint32_t)(g.G / NCTR + (lane < g.G % NCTR ? 1 : 0)) : 0u;
+    uint32_t* a = g.bar + ((size_t)k * NCTR + c) * CTR_STRIDE;
     const unsigned long long t0 = wall_clock64();
     while (true) {
       const uint32_t v = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__all(v >= need)) break;
-      const uint32_t e = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t e = __hip_atomic_load(g.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (e & MK_DEVERR_BARRIER) break;
-      if (wall_clock64() - t0 > timeout) {
+      if (wall_clock64() - t0 > g.timeout) {
         if (lane == 0)
-          __hip_atomic_fetch_or(err, MK_DEVERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_or(g.err, MK_DEVERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-__device__ __forceinline__ void grid_wait(Grid& g) { grid_wait_k(g.bar, g.err, g.G, g.k - 1, g.timeout); }
+// Wait on the latest barrier this workgroup arrived at.
+__device__ __forceinline__ void grid_wait(Grid& g) {
+  grid_wait_k(g, g.k - 1);
+  trace_mark(g, 2 * g.k);
+}
 
 // ---------------------------------------------------------------------------
 // Row streams: a wave's share of a GEMV, software pipelined through a ring of
@@ -336,15 +375,17 @@ struct Ctx {
   const KParams* p;
   Grid g;
   int pos;
-  int n_rows;           // KV rows attended: pos + 1
-  const uint16_t* x_in; // layer input of the first layer (embedding row or hidden_in)
-  uint16_t* hA;
-  uint16_t* hB;
-  uint16_t* qv;
-  uint16_t* att;
-  uint16_t* act;
+  int n_rows;            // KV rows attended: pos + 1
+  const uint16_t* x_in;  // input of the first layer (embedding row or hidden_in)
+  uint8_t* acts;         // per-layer activation buffers
   float* part;
   uint32_t* misc;
+
+  __device__ __forceinline__ uint16_t* buf(int li, size_t which) const {
+    return reinterpret_cast<uint16_t*>(acts + (size_t)li * ACT_LAYER_BYTES + which);
+  }
+  // layer input: the previous layer's h2, or the step input for the first layer
+  __device__ __forceinline__ const uint16_t* h_in(int li) const { return li == 0 ? x_in : buf(li - 1, ACT_H2); }
 };
 
 __device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rrow, int d) {
@@ -357,9 +398,10 @@ __device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rro
   return u32x4{f2bf(ra), f2bf(rb), 0u, 0u};
 }
 
-// QKV phase of layer l (layer index into the stacks).
-__device__ __forceinline__ void phase_qkv(Ctx& c, int l, bool first, float* s_val) {
+// QKV phase of run-layer li (stack layer l): RMSNorm, GEMV, RoPE, q out, K/V rows in place.
+__device__ __forceinline__ void phase_qkv(Ctx& c, int li, float* s_val) {
   const KParams& p = *c.p;
+  const int l = p.first_layer + li;
   const int G = c.g.G, w = c.g.wg, wave = wave_id();
   int P0, P1;
   share(QKV_PAIRS, G, w, P0, P1);
@@ -367,9 +409,9 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int l, bool first, float* s_va
   RowStream<4, 4> rs;
   rs.start(make_rsrc(p.w_qkv + (size_t)l * QKV_ROWS * H, QKV_LAYER_BYTES),
            (uint32_t)(2 * P0 + wave) * (H * 2), NWAVE * H * 2, wave_count(0, nrows));
-  if (!first) grid_wait(c.g);
+  if (li > 0) grid_wait(c.g);
   u32x4 xs[4];
-  load_x2048(first ? c.x_in : c.hA, xs);
+  load_x2048(c.h_in(li), xs);
   rmsnorm2048(xs, nullptr);
   rs.run([&](const u32x4(&wv)[4]) {
            float a = dot8(wv[0], xs[0], 0.f);
@@ -384,31 +426,29 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int l, bool first, float* s_va
          });
   __syncthreads();
   const uint16_t* rrow = p.rope + (size_t)c.pos * (2 * HD);
+  uint16_t* qv = c.buf(li, ACT_Q);
   for (int lp = threadIdx.x; lp < P1 - P0; lp += NT) {
     const int pr = P0 + lp;
     const float a = rbf(s_val[2 * lp]), b = rbf(s_val[2 * lp + 1]);
+    uint16_t* dst;
+    u32x4 o;
     if (pr < Q_PAIRS) {
-      const int head = pr >> 5, d = pr & 31;
-      const u32x4 o = rope_pair(a, b, rrow, d);
-      c.qv[head * HD + d] = (uint16_t)o.x;
-      c.qv[head * HD + d + 32] = (uint16_t)o.y;
+      dst = qv + (pr >> 5) * HD;
+      o = rope_pair(a, b, rrow, pr & 31);
     } else if (pr < Q_PAIRS + K_PAIRS) {
-      const int kvh = (pr - Q_PAIRS) >> 5, d = pr & 31;
-      const u32x4 o = rope_pair(a, b, rrow, d);
-      uint16_t* row = p.kc[l - p.first_layer] + ((size_t)kvh * p.s_max + c.pos) * HD;
-      row[d] = (uint16_t)o.x;
-      row[d + 32] = (uint16_t)o.y;
+      dst = p.kc[li] + ((size_t)((pr - Q_PAIRS) >> 5) * p.s_max + c.pos) * HD;
+      o = rope_pair(a, b, rrow, pr & 31);
     } else {
-      const int kvh = (pr - Q_PAIRS - K_PAIRS) >> 5, d = pr & 31;
-      uint16_t* row = p.vc[l - p.first_layer] + ((size_t)kvh * p.s_max + c.pos) * HD;
-      row[d] = (uint16_t)f2bf(a);
-      row[d + 32] = (uint16_t)f2bf(b);
+      dst = p.vc[li] + ((size_t)((pr - Q_PAIRS - K_PAIRS) >> 5) * p.s_max + c.pos) * HD;
+      o = u32x4{f2bf(a), f2bf(b), 0u, 0u};
     }
+    st_dev(dst + (pr & 31), o.x);
+    st_dev(dst + (pr & 31) + 32, o.y);
   }
   grid_arrive(c.g);
 }
 
-// One attention work item: kv head h, rows [s*ATT_ROWS, ...) of [0, n_rows).
+// One attention work item: kv head h, KV rows [s*ATT_ROWS, ...) of [0, n_rows).
 struct AttnShared {
   float mx[NWAVE][GQA];
   float sm[NWAVE][GQA];
@@ -416,22 +456,25 @@ struct AttnShared {
   int last;
 };
 
-__device__ __forceinline__ void attn_item(Ctx& c, int l, int h, int s, int nsplit, AttnShared& sh) {
+__device__ __forceinline__ void attn_item(Ctx& c, int li, int h, int s, int nsplit, AttnShared& sh) {
   const KParams& p = *c.p;
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id();
   const int j0 = s * ATT_ROWS;
   const int rows_here = min(ATT_ROWS, c.n_rows - j0);
   const bool va = rl < rows_here, vb = rl + 32 < rows_here;
   const int ja = j0 + (va ? rl : 0), jb = j0 + (vb ? rl + 32 : 0);
-  const uint16_t* Kh = p.kc[l - p.first_layer] + (size_t)h * p.s_max * HD;
-  const uint16_t* Vh = p.vc[l - p.first_layer] + (size_t)h * p.s_max * HD;
-  const u32x4 ka = *reinterpret_cast<const u32x4*>(Kh + (size_t)ja * HD + ch * 8);
-  const u32x4 kb = *reinterpret_cast<const u32x4*>(Kh + (size_t)jb * HD + ch * 8);
-  const u32x4 vA = *reinterpret_cast<const u32x4*>(Vh + (size_t)ja * HD + ch * 8);
-  const u32x4 vB = *reinterpret_cast<const u32x4*>(Vh + (size_t)jb * HD + ch * 8);
+  // this head's K and V rows, read with device-scope loads (row pos was written this launch)
+  const size_t head_bytes = (size_t)p.s_max * HD * 2;
+  const rsrc_t rk = make_rsrc(p.kc[li] + (size_t)h * p.s_max * HD, head_bytes);
+  const rsrc_t rv = make_rsrc(p.vc[li] + (size_t)h * p.s_max * HD, head_bytes);
+  const u32x4 ka = ld_dev16(rk, (uint32_t)(ja * HD + ch * 8) * 2u);
+  const u32x4 kb = ld_dev16(rk, (uint32_t)(jb * HD + ch * 8) * 2u);
+  const u32x4 vA = ld_dev16(rv, (uint32_t)(ja * HD + ch * 8) * 2u);
+  const u32x4 vB = ld_dev16(rv, (uint32_t)(jb * HD + ch * 8) * 2u);
+  const uint16_t* qv = c.buf(li, ACT_Q);
   u32x4 q[GQA];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(c.qv + (h * GQA + g) * HD + ch * 8);
+  for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(qv + (h * GQA + g) * HD + ch * 8);
   float sa[GQA], sb[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
@@ -442,7 +485,7 @@ __device__ __forceinline__ void attn_item(Ctx& c, int l, int h, int s, int nspli
     sa[g] = va ? x * SM_SCALE : -INFINITY;
     sb[g] = vb ? y * SM_SCALE : -INFINITY;
   }
-  // row max over the item (lanes of one row hold equal values)
+  // max over the item's rows (the 8 lanes of one row hold equal values)
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
     float m = fmaxf(sa[g], sb[g]);
@@ -452,19 +495,19 @@ __device__ __forceinline__ void attn_item(Ctx& c, int l, int h, int s, int nspli
     if (lane_id() == 0) sh.mx[wave][g] = m;
   }
   __syncthreads();
-  float pa[GQA], pb[GQA], mg[GQA];
+  float pa[GQA], pb[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
-    mg[g] = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
-    pa[g] = va ? __expf(sa[g] - mg[g]) : 0.f;
-    pb[g] = vb ? __expf(sb[g] - mg[g]) : 0.f;
+    const float mg = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
+    pa[g] = va ? __expf(sa[g] - mg) : 0.f;
+    pb[g] = vb ? __expf(sb[g] - mg) : 0.f;
     float sum = pa[g] + pb[g];
     sum += __shfl_xor(sum, 8, 64);
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     if (lane_id() == 0) sh.sm[wave][g] = sum;
   }
-  // PV: this lane's 8 dims (ch*8..) for its two rows, all 4 heads
+  // PV for this lane's 8 dims (ch*8..) over its two rows, all 4 heads of the group
   float acc[GQA][8];
   const uint32_t va_w[4] = {vA.x, vA.y, vA.z, vA.w};
   const uint32_t vb_w[4] = {vB.x, vB.y, vB.z, vB.w};
@@ -501,37 +544,38 @@ __device__ __forceinline__ void attn_item(Ctx& c, int l, int h, int s, int nspli
     float o = 0.f;
 #pragma unroll
     for (int wv = 0; wv < NWAVE; ++wv) o += sh.pv[wv][d >> 3][g * 8 + (d & 7)];
-    part[2 * GQA + g * HD + d] = o;
+    st_dev(part + 2 * GQA + g * HD + d, o);
     if (t < GQA) {
-      part[t] = fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t]));
-      part[GQA + t] = sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t];
+      st_dev(part + t, fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t])));
+      st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
     }
   }
+  // completion count for this head; the last split to finish merges
+  wait_mem();
   __syncthreads();
   if (t == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(c.misc + MISC_HEAD + h, 1u, __ATOMIC_ACQ_REL,
+    const uint32_t prev = __hip_atomic_fetch_add(c.misc + MISC_HEAD + h, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     sh.last = (prev == (uint32_t)(nsplit - 1));
   }
   __syncthreads();
   if (!sh.last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   {
-    // merge the nsplit partials of this kv head: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s
+    // o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s  over the nsplit partials of this kv head
     const int g = t >> 6, d = t & 63;
     const float* base = c.part + (size_t)h * p.max_split * PART_FLOATS;
     float M = -INFINITY;
-    for (int k = 0; k < nsplit; ++k) M = fmaxf(M, base[(size_t)k * PART_FLOATS + g]);
+    for (int k = 0; k < nsplit; ++k) M = fmaxf(M, ld_dev(base + (size_t)k * PART_FLOATS + g));
     float L = 0.f, O = 0.f;
     for (int k = 0; k < nsplit; ++k) {
       const float* pk = base + (size_t)k * PART_FLOATS;
-      const float f = __expf(pk[g] - M);
-      L = fmaf(f, pk[GQA + g], L);
-      O = fmaf(f, pk[2 * GQA + g * HD + d], O);
+      const float f = __expf(ld_dev(pk + g) - M);
+      L = fmaf(f, ld_dev(pk + GQA + g), L);
+      O = fmaf(f, ld_dev(pk + 2 * GQA + g * HD + d), O);
     }
-    c.att[(h * GQA + g) * HD + d] = (uint16_t)f2bf(O * (1.0f / L));
+    st_dev(c.buf(li, ACT_ATT) + (h * GQA + g) * HD + d, f2bf(O * (1.0f / L)));
   }
-  if (t == 0) c.misc[MISC_HEAD + h] = 0u;
+  if (t == 0) __hip_atomic_store(c.misc + MISC_HEAD + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
@@ -550,11 +594,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   c.g.wg = blockIdx.x;
   c.g.k = 0;
   c.g.timeout = p.timeout_ticks;
-  c.hA = reinterpret_cast<uint16_t*>(p.ws + OFF_HA);
-  c.hB = reinterpret_cast<uint16_t*>(p.ws + OFF_HB);
-  c.qv = reinterpret_cast<uint16_t*>(p.ws + OFF_Q);
-  c.att = reinterpret_cast<uint16_t*>(p.ws + OFF_ATT);
-  c.act = reinterpret_cast<uint16_t*>(p.ws + OFF_ACT);
+  c.g.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
+  trace_mark(c.g, 0);
+  c.acts = p.ws + OFF_ACTS;
   c.part = reinterpret_cast<float*>(p.ws + OFF_PART);
   c.pos = p.pos[0];
   const bool pos_ok = c.pos >= 0 && c.pos < p.s_max && c.pos < p.rope_rows;
@@ -571,32 +613,38 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   const int G = c.g.G, w = c.g.wg, wave = wave_id(), lane = lane_id();
 
   if (pos_ok) {
+    int R0, R1;
+    share(H, G, w, R0, R1);
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
-      const bool first = li == 0;
       const bool last = li == p.n_layers - 1;
-      phase_qkv(c, l, first, s_val);
+      phase_qkv(c, li, s_val);
 
-      // ---- attention (O-projection weights prefetched first) ----
-      int R0, R1;
-      share(H, G, w, R0, R1);
+      // ---- attention; the O-projection weights are prefetched meanwhile ----
       RowStream<2, 4> os;
-      os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)(R0 + wave) * (H * 2),
-               NWAVE * H * 2, wave_count(R0, R1));
-      grid_wait(c.g);
-      {
-        const int nsplit = (c.n_rows + ATT_ROWS - 1) / ATT_ROWS;
-        const int nitems = NKV * nsplit;
-        for (int it = w; it < nitems; it += G) attn_item(c, l, it / nsplit, it % nsplit, nsplit, s_att);
+      const int nsplit = (c.n_rows + ATT_ROWS - 1) / ATT_ROWS;
+      const int nitems = NKV * nsplit;
+      if (w < nitems) {
+        os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)(R0 + wave) * (H * 2),
+                 NWAVE * H * 2, wave_count(R0, R1));
+        grid_wait(c.g);
+        for (int it = w; it < nitems; it += G) attn_item(c, li, it / nsplit, it % nsplit, nsplit, s_att);
+        grid_arrive(c.g);
+      } else {
+        // no attention work: arrive at once without waiting on the QKV
+        // barrier (each barrier has its own counters, so arriving early is safe)
+        grid_arrive(c.g);
+        os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)(R0 + wave) * (H * 2),
+                 NWAVE * H * 2, wave_count(R0, R1));
       }
-      grid_arrive(c.g);
 
-      // ---- O projection + residual ----
+      // ---- O projection + residual -> h1 ----
       grid_wait(c.g);
       {
         u32x4 xs[4];
-        load_x2048(c.att, xs);
-        const uint16_t* hprev = first ? c.x_in : c.hA;
+        load_x2048(c.buf(li, ACT_ATT), xs);
+        const uint16_t* hprev = c.h_in(li);
+        uint16_t* h1 = c.buf(li, ACT_H1);
         os.run([&](const u32x4(&wv)[4]) {
                  float a = dot8(wv[0], xs[0], 0.f);
                  float b = dot8(wv[1], xs[1], 0.f);
@@ -608,13 +656,13 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  const float v = wave_sum(part);
                  if (lane == 0) {
                    const int row = R0 + wave + NWAVE * r;
-                   c.hB[row] = (uint16_t)f2bf(bf2f(hprev[row]) + rbf(v));
+                   st_dev(h1 + row, f2bf(bf2f(hprev[row]) + rbf(v)));
                  }
                });
       }
       grid_arrive(c.g);
 
-      // ---- gate/up + SwiGLU ----
+      // ---- gate/up + SwiGLU -> act ----
       {
         int U0, U1;
         share(INTER, G, w, U0, U1);
@@ -623,8 +671,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  (uint32_t)(U0 + wave) * (2 * H * 2), NWAVE * 2 * H * 2, wave_count(U0, U1));
         grid_wait(c.g);
         u32x4 xs[4];
-        load_x2048(c.hB, xs);
+        load_x2048(c.buf(li, ACT_H1), xs);
         rmsnorm2048(xs, nullptr);
+        uint16_t* act = c.buf(li, ACT_ACT);
         struct GU2 { float g, u; };
         gs.run([&](const u32x4(&wv)[8]) {
                  float g0 = dot8(wv[0], xs[0], 0.f), g1 = dot8(wv[1], xs[1], 0.f);
@@ -640,21 +689,24 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  const float uv = wave_sum(part.u);
                  if (lane == 0) {
                    const float silu = gv / (1.0f + __expf(-gv));
-                   c.act[U0 + wave + NWAVE * r] = (uint16_t)f2bf(silu * uv);
+                   st_dev(act + U0 + wave + NWAVE * r, f2bf(silu * uv));
                  }
                });
       }
       grid_arrive(c.g);
 
-      // ---- down projection + residual ----
+      // ---- down projection + residual -> h2 ----
       {
         RowStream<2, 16> ds;
         ds.start(make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES), (uint32_t)(R0 + wave) * (INTER * 2),
                  NWAVE * INTER * 2, wave_count(R0, R1));
         grid_wait(c.g);
+        const uint16_t* act = c.buf(li, ACT_ACT);
+        const uint16_t* h1 = c.buf(li, ACT_H1);
+        uint16_t* h2 = c.buf(li, ACT_H2);
         u32x4 xs[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xs[i] = *reinterpret_cast<const u32x4*>(c.act + i * 512 + lane * 8);
+        for (int i = 0; i < 16; ++i) xs[i] = *reinterpret_cast<const u32x4*>(act + i * 512 + lane * 8);
         ds.run([&](const u32x4(&wv)[16]) {
                  float a = 0.f, b = 0.f;
 #pragma unroll
@@ -668,9 +720,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  const float v = wave_sum(part);
                  if (lane == 0) {
                    const int row = R0 + wave + NWAVE * r;
-                   const uint16_t h2 = (uint16_t)f2bf(bf2f(c.hB[row]) + rbf(v));
-                   c.hA[row] = h2;
-                   if (last && p.hidden_out) p.hidden_out[row] = h2;
+                   const uint32_t hv = f2bf(bf2f(h1[row]) + rbf(v));
+                   st_dev(h2 + row, hv);
+                   if (last && p.hidden_out) p.hidden_out[row] = (uint16_t)hv;
                  }
                });
       }
@@ -686,7 +738,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                wave_count(V0, V1));
       grid_wait(c.g);
       u32x4 xs[4];
-      load_x2048(c.hA, xs);
+      load_x2048(c.buf(p.n_layers - 1, ACT_H2), xs);
       rmsnorm2048(xs, p.g_final);
       float best = -INFINITY;
       int bidx = 0x7fffffff;
@@ -732,22 +784,23 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   }
 
   // ---- exit: the last workgroup out finalises and resets the control block ----
+  trace_mark(c.g, MK_TRACE_SLOTS - 1);
+  wait_mem();
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
-        __hip_atomic_fetch_add(c.misc + MISC_EXIT, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(c.misc + MISC_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (uint32_t)(G - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   for (int i = threadIdx.x; i < c.g.k * NCTR; i += NT) c.g.bar[(size_t)i * CTR_STRIDE] = 0u;
   if (threadIdx.x == 0) {
     c.misc[MISC_EXIT] = 0u;
     if (pos_ok) {
       if (p.do_lm) {
         unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + OFF_MISC + MISC_KEY_BYTE);
-        const unsigned long long key = *kp;
+        const unsigned long long key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *kp = 0ull;
         if (p.next_token) p.next_token[0] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
       }
@@ -822,6 +875,12 @@ int mk_grid_size(int device) {
   DeviceInfo d;
   const int rc = device_info(device, &d);
   return rc == MK_OK ? d.grid : rc;
+}
+
+long long mk_wall_clock_hz(int device) {
+  DeviceInfo d;
+  const int rc = device_info(device, &d);
+  return rc == MK_OK ? (long long)d.ticks_per_s : rc;
 }
 
 size_t mk_workspace_bytes(int32_t batch, int32_t s_max) {
@@ -923,6 +982,7 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   kp.flags = a->flags;
   kp.max_split = max_split_for(a->s_max);
   kp.timeout_ticks = di.ticks_per_s * 2ull;   // 2 s per barrier wait
+  kp.trace = static_cast<unsigned long long*>(a->trace);
 
   void* args[] = {&kp};
   const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid),

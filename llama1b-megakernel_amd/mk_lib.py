@@ -44,7 +44,7 @@ class MkStepArgs(ctypes.Structure):
         ("tokens", c_void_p), ("hidden_in", c_void_p), ("pos", c_void_p),
         ("hidden_out", c_void_p), ("logits", c_void_p), ("next_token", c_void_p),
         ("flags", c_uint32), ("workspace", c_void_p), ("workspace_bytes", c_size_t),
-        ("stream", c_void_p),
+        ("stream", c_void_p), ("trace", c_void_p),
     ]
 
 
@@ -68,6 +68,8 @@ def load() -> ctypes.CDLL:
         lib.mk_last_error.restype = c_char_p
         lib.mk_grid_size.argtypes = [c_int]
         lib.mk_grid_size.restype = c_int
+        lib.mk_wall_clock_hz.argtypes = [c_int]
+        lib.mk_wall_clock_hz.restype = ctypes.c_longlong
         lib.mk_workspace_bytes.argtypes = [c_int32, c_int32]
         lib.mk_workspace_bytes.restype = c_size_t
         lib.mk_workspace_init.argtypes = [c_void_p, c_size_t, c_void_p]
@@ -134,7 +136,8 @@ def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tens
                 tokens: Optional[torch.Tensor] = None, hidden_in: Optional[torch.Tensor] = None,
                 hidden_out: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None,
                 next_token: Optional[torch.Tensor] = None, first_layer: int = 0,
-                n_layers: Optional[int] = None, flags: int = 0, batch: int = 1) -> None:
+                n_layers: Optional[int] = None, flags: int = 0, batch: int = 1,
+                trace: Optional[torch.Tensor] = None) -> None:
     """One call of ``mk_decode_step`` on the current torch stream."""
     n = len(k_caches) if n_layers is None else n_layers
     if len(k_caches) < n or len(v_caches) < n:
@@ -145,8 +148,42 @@ def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tens
     a = MkStepArgs(first_layer, n, batch, s_max, ctypes.cast(kc, POINTER(c_void_p)),
                    ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes,
-                   current_stream_ptr())
+                   current_stream_ptr(), _ptr(trace))
     check(load().mk_decode_step(ctypes.byref(weights), ctypes.byref(a)))
+
+
+class StepLauncher:
+    """A prebuilt ``mk_decode_step`` call: the argument struct is built once and
+    every ``launch()`` enqueues the same step on the stream. With
+    ``next_token`` aliasing ``tokens`` and ``MK_FLAG_ADVANCE`` the launches form
+    an autoregressive loop that needs no host work between steps."""
+
+    def __init__(self, weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tensor],
+                 v_caches: Sequence[torch.Tensor], pos: torch.Tensor, *,
+                 tokens: Optional[torch.Tensor] = None, hidden_in: Optional[torch.Tensor] = None,
+                 hidden_out: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None,
+                 next_token: Optional[torch.Tensor] = None, first_layer: int = 0,
+                 n_layers: Optional[int] = None, flags: int = 0, batch: int = 1,
+                 stream: Optional[torch.cuda.Stream] = None, trace: Optional[torch.Tensor] = None):
+        n = len(k_caches) if n_layers is None else n_layers
+        self._keep = (weights, ws, list(k_caches), list(v_caches), pos, tokens, hidden_in, hidden_out,
+                      logits, next_token, trace)
+        self._kc = (c_void_p * n)(*[t.data_ptr() for t in k_caches[:n]])
+        self._vc = (c_void_p * n)(*[t.data_ptr() for t in v_caches[:n]])
+        st = (stream or torch.cuda.current_stream()).cuda_stream
+        self.args = MkStepArgs(first_layer, n, batch, int(k_caches[0].shape[-2]),
+                               ctypes.cast(self._kc, POINTER(c_void_p)), ctypes.cast(self._vc, POINTER(c_void_p)),
+                               _ptr(tokens), _ptr(hidden_in), _ptr(pos), _ptr(hidden_out), _ptr(logits),
+                               _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes, st, _ptr(trace))
+        self.weights = weights
+        self._fn = load().mk_decode_step
+        self._wref = ctypes.byref(self.weights)
+        self._aref = ctypes.byref(self.args)
+
+    def launch(self) -> None:
+        rc = self._fn(self._wref, self._aref)
+        if rc != MK_OK:
+            check(rc)
 
 
 def header_functions(header: Path) -> List[str]:
