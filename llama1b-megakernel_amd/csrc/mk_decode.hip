@@ -65,7 +65,8 @@ constexpr int Q_PAIRS = NQ * HD / 2;       // 1024
 constexpr int K_PAIRS = NKV * HD / 2;      // 256
 constexpr int NT = 256;                    // threads per workgroup
 constexpr int NWAVE = NT / 64;
-constexpr int ATT_ROWS = 64;               // KV rows per attention work item
+constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
+constexpr int ATT_GROUP = 128;             // KV rows an attention item loads at once (4 rounds of 32)
 constexpr int NCTR = 8;                    // arrival counters per grid barrier
 constexpr int MAX_BARRIERS = 5 * MK_MAX_LAYERS + 4;
 constexpr int CTR_STRIDE = 32;             // u32 words between counters (128 B)
@@ -85,20 +86,20 @@ constexpr size_t EMBED_BYTES = (size_t)VOCAB * H * 2;
 // Workspace layout (bytes, batch 1).
 constexpr size_t OFF_BAR = 0;
 constexpr size_t BAR_BYTES = (size_t)MAX_BARRIERS * NCTR * CTR_STRIDE * 4;
-constexpr size_t OFF_MISC = BAR_BYTES;                 // exit counter, error bits, head counters, argmax key
-constexpr size_t MISC_EXIT = 0, MISC_ERR = 1, MISC_HEAD = 16;   // u32 indices
+constexpr size_t OFF_MISC = BAR_BYTES;                 // exit counter, error bits, argmax key
+constexpr size_t MISC_EXIT = 0, MISC_ERR = 1;                   // u32 indices
 constexpr size_t MISC_KEY_BYTE = 128;                           // u64
 // Activation buffers, one set per layer (each written once per launch):
 //   h1 [2048] | q [2048] | att [2048] | act [8192] | h2 [2048]   (bf16)
 constexpr size_t ACT_H1 = 0, ACT_Q = H * 2, ACT_ATT = 2 * H * 2, ACT_ACT = 3 * H * 2,
                  ACT_H2 = 3 * H * 2 + INTER * 2, ACT_LAYER_BYTES = 4 * H * 2 + INTER * 2;
 constexpr size_t OFF_ACTS = OFF_MISC + 256;
+// Split-K attention partials, one set per layer: [layer][kv head][split][m(4) l(4) o(4x64)] fp32.
 constexpr size_t OFF_PART = OFF_ACTS + (size_t)MK_MAX_LAYERS * ACT_LAYER_BYTES;
+constexpr size_t PART_LAYER_FLOATS = (size_t)NKV * ATT_MAX_SPLIT * PART_FLOATS;
+constexpr size_t WS_BYTES = OFF_PART + (size_t)MK_MAX_LAYERS * PART_LAYER_FLOATS * 4;
 
-inline int max_split_for(int s_max) { return (s_max + ATT_ROWS - 1) / ATT_ROWS; }
-inline size_t ws_bytes_for(int s_max) {
-  return OFF_PART + (size_t)NKV * max_split_for(s_max) * PART_FLOATS * 4;
-}
+inline size_t ws_bytes_for(int) { return WS_BYTES; }
 
 // ---------------------------------------------------------------------------
 // Device helpers
@@ -208,7 +209,6 @@ struct KParams {
   int rope_rows;
   int do_lm;
   uint32_t flags;
-  int max_split;
   unsigned long long timeout_ticks;
   unsigned long long* trace;
 };
@@ -448,97 +448,117 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, float* s_val) {
   grid_arrive(c.g);
 }
 
-// One attention work item: kv head h, KV rows [s*ATT_ROWS, ...) of [0, n_rows).
+// One attention work item: kv head h, KV rows [j0, j1) of [0, n_rows), for the
+// 4 q heads of the group (GQA). Thread t serves row (t >> 3) of each 32-row
+// round and the 8 dims (t & 7)*8.. of it; rows stream in groups of
+// ATT_GROUP with an online softmax. Writes the item's partial
+// (m[4], l[4], o[4][64]) unnormalised, relative to m.
 struct AttnShared {
   float mx[NWAVE][GQA];
   float sm[NWAVE][GQA];
   float pv[NWAVE][8][GQA * 8];
-  int last;
 };
 
-__device__ __forceinline__ void attn_item(Ctx& c, int li, int h, int s, int nsplit, AttnShared& sh) {
+__device__ __forceinline__ void attn_item(Ctx& c, int li, int h, int j0, int j1, float* part, AttnShared& sh) {
   const KParams& p = *c.p;
-  const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id();
-  const int j0 = s * ATT_ROWS;
-  const int rows_here = min(ATT_ROWS, c.n_rows - j0);
-  const bool va = rl < rows_here, vb = rl + 32 < rows_here;
-  const int ja = j0 + (va ? rl : 0), jb = j0 + (vb ? rl + 32 : 0);
-  // this head's K and V rows, read with device-scope loads (row pos was written this launch)
+  const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
+  // this head's K and V rows, device-scope loads (row pos was written in this launch)
   const size_t head_bytes = (size_t)p.s_max * HD * 2;
   const rsrc_t rk = make_rsrc(p.kc[li] + (size_t)h * p.s_max * HD, head_bytes);
   const rsrc_t rv = make_rsrc(p.vc[li] + (size_t)h * p.s_max * HD, head_bytes);
-  const u32x4 ka = ld_dev16(rk, (uint32_t)(ja * HD + ch * 8) * 2u);
-  const u32x4 kb = ld_dev16(rk, (uint32_t)(jb * HD + ch * 8) * 2u);
-  const u32x4 vA = ld_dev16(rv, (uint32_t)(ja * HD + ch * 8) * 2u);
-  const u32x4 vB = ld_dev16(rv, (uint32_t)(jb * HD + ch * 8) * 2u);
   const uint16_t* qv = c.buf(li, ACT_Q);
   u32x4 q[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(qv + (h * GQA + g) * HD + ch * 8);
-  float sa[GQA], sb[GQA];
+  float m_run[GQA], l_run[GQA], acc[GQA][8];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
-    float x = dot8(ka, q[g], 0.f), y = dot8(kb, q[g], 0.f);
-    x += __shfl_xor(x, 1, 64); y += __shfl_xor(y, 1, 64);
-    x += __shfl_xor(x, 2, 64); y += __shfl_xor(y, 2, 64);
-    x += __shfl_xor(x, 4, 64); y += __shfl_xor(y, 4, 64);
-    sa[g] = va ? x * SM_SCALE : -INFINITY;
-    sb[g] = vb ? y * SM_SCALE : -INFINITY;
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  // max over the item's rows (the 8 lanes of one row hold equal values)
+  constexpr int R = ATT_GROUP / 32;
+  for (int base = j0; base < j1; base += ATT_GROUP) {
+    u32x4 kk[R], vv[R];
+    bool valid[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = base + 32 * r + rl;
+      valid[r] = j < j1;
+      const uint32_t off = valid[r] ? (uint32_t)(j * HD + ch * 8) * 2u : OOB;
+      kk[r] = ld_dev16(rk, off);
+      vv[r] = ld_dev16(rv, off);
+    }
+    float sc[R][GQA];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int g = 0; g < GQA; ++g) {
+        float x = dot8(kk[r], q[g], 0.f);
+        x += __shfl_xor(x, 1, 64);
+        x += __shfl_xor(x, 2, 64);
+        x += __shfl_xor(x, 4, 64);
+        sc[r][g] = valid[r] ? x * SM_SCALE : -INFINITY;
+      }
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      float mn = m_run[g];
+#pragma unroll
+      for (int r = 0; r < R; ++r) mn = fmaxf(mn, sc[r][g]);
+      const float keep = mn == -INFINITY ? 1.f : __expf(m_run[g] - mn);
+      l_run[g] *= keep;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float pr = valid[r] ? __expf(sc[r][g] - mn) : 0.f;
+        l_run[g] += pr;
+        const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[g][2 * e] = fmaf(pr, bf_lo(w4[e]), acc[g][2 * e]);
+          acc[g][2 * e + 1] = fmaf(pr, bf_hi(w4[e]), acc[g][2 * e + 1]);
+        }
+      }
+      m_run[g] = mn;
+    }
+  }
+  // merge the 32 row-lanes of the item: max, rescale, sum (lanes of one row agree)
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
-    float m = fmaxf(sa[g], sb[g]);
+    float m = m_run[g];
     m = fmaxf(m, __shfl_xor(m, 8, 64));
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if (lane_id() == 0) sh.mx[wave][g] = m;
+    if (lane == 0) sh.mx[wave][g] = m;
   }
   __syncthreads();
-  float pa[GQA], pb[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
-    const float mg = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
-    pa[g] = va ? __expf(sa[g] - mg) : 0.f;
-    pb[g] = vb ? __expf(sb[g] - mg) : 0.f;
-    float sum = pa[g] + pb[g];
-    sum += __shfl_xor(sum, 8, 64);
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    if (lane_id() == 0) sh.sm[wave][g] = sum;
-  }
-  // PV for this lane's 8 dims (ch*8..) over its two rows, all 4 heads of the group
-  float acc[GQA][8];
-  const uint32_t va_w[4] = {vA.x, vA.y, vA.z, vA.w};
-  const uint32_t vb_w[4] = {vB.x, vB.y, vB.z, vB.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a0 = bf_lo(va_w[e]), a1 = bf_hi(va_w[e]);
-    const float b0 = bf_lo(vb_w[e]), b1 = bf_hi(vb_w[e]);
-#pragma unroll
-    for (int g = 0; g < GQA; ++g) {
-      acc[g][2 * e] = fmaf(pa[g], a0, pb[g] * b0);
-      acc[g][2 * e + 1] = fmaf(pa[g], a1, pb[g] * b1);
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < GQA; ++g)
+    const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
+    const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
+    float l = l_run[g] * f;
+    l += __shfl_xor(l, 8, 64);
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (lane == 0) sh.sm[wave][g] = l;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float v = acc[g][e];
+      float v = acc[g][e] * f;
       v += __shfl_xor(v, 8, 64);
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
       acc[g][e] = v;
     }
-  if (lane_id() < 8) {
+  }
+  if (lane < 8) {
 #pragma unroll
     for (int g = 0; g < GQA; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) sh.pv[wave][ch][g * 8 + e] = acc[g][e];
   }
   __syncthreads();
-  float* part = c.part + ((size_t)h * p.max_split + s) * PART_FLOATS;
   {
     const int g = t >> 6, d = t & 63;
     float o = 0.f;
@@ -550,37 +570,68 @@ __device__ __forceinline__ void attn_item(Ctx& c, int li, int h, int s, int nspl
       st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
     }
   }
-  // completion count for this head; the last split to finish merges
-  wait_mem();
-  __syncthreads();
-  if (t == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(c.misc + MISC_HEAD + h, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = (prev == (uint32_t)(nsplit - 1));
+  __syncthreads();   // LDS reuse by a following item
+}
+
+// Split of [0, n_rows) into nsplit items of `rows` rows (a multiple of 32).
+__device__ __forceinline__ void attn_split(int n_rows, int& nsplit, int& rows) {
+  int ns = (n_rows + 31) / 32;
+  ns = ns < ATT_MAX_SPLIT ? ns : ATT_MAX_SPLIT;
+  rows = ((n_rows + ns - 1) / ns + 31) / 32 * 32;
+  nsplit = (n_rows + rows - 1) / rows;
+}
+
+// Merge the split-K partials of all 32 q heads into bf16 att in LDS:
+//   att = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s   (then cast to bf16)
+// Thread t produces q head t>>3, dims (t&7)*8 .. +7.
+__device__ __forceinline__ void attn_merge(const float* part_layer, int nsplit, uint16_t* att_lds) {
+  const int t = threadIdx.x, qh = t >> 3, d0 = (t & 7) * 8, h = qh >> 2, g = qh & 3;
+  // all loads issued at once; splits >= nsplit read zero through out-of-range offsets
+  const rsrc_t r = make_rsrc(part_layer + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS,
+                             (size_t)nsplit * PART_FLOATS * 4);
+  u32x4 ml[ATT_MAX_SPLIT][2], oa[ATT_MAX_SPLIT], ob[ATT_MAX_SPLIT];
+#pragma unroll
+  for (int s = 0; s < ATT_MAX_SPLIT; ++s) {
+    const uint32_t base = (uint32_t)(s * PART_FLOATS) * 4u;
+    ml[s][0] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)base, 0, 0);          // m[0..3]
+    ml[s][1] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(base + 16u), 0, 0);  // l[0..3]
+    const uint32_t o = base + (uint32_t)(2 * GQA + g * HD + d0) * 4u;
+    oa[s] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)o, 0, 0);
+    ob[s] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(o + 16u), 0, 0);
   }
-  __syncthreads();
-  if (!sh.last) return;
-  {
-    // o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s  over the nsplit partials of this kv head
-    const int g = t >> 6, d = t & 63;
-    const float* base = c.part + (size_t)h * p.max_split * PART_FLOATS;
-    float M = -INFINITY;
-    for (int k = 0; k < nsplit; ++k) M = fmaxf(M, ld_dev(base + (size_t)k * PART_FLOATS + g));
-    float L = 0.f, O = 0.f;
-    for (int k = 0; k < nsplit; ++k) {
-      const float* pk = base + (size_t)k * PART_FLOATS;
-      const float f = __expf(ld_dev(pk + g) - M);
-      L = fmaf(f, ld_dev(pk + GQA + g), L);
-      O = fmaf(f, ld_dev(pk + 2 * GQA + g * HD + d), O);
-    }
-    st_dev(c.buf(li, ACT_ATT) + (h * GQA + g) * HD + d, f2bf(O * (1.0f / L)));
+  auto pick = [g](u32x4 v) { return __uint_as_float(g == 0 ? v.x : g == 1 ? v.y : g == 2 ? v.z : v.w); };
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < ATT_MAX_SPLIT; ++s)
+    if (s < nsplit) M = fmaxf(M, pick(ml[s][0]));
+  float O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+#pragma unroll
+  for (int s = 0; s < ATT_MAX_SPLIT; ++s) {
+    const float w = s < nsplit ? __expf(pick(ml[s][0]) - M) : 0.f;
+    L = fmaf(w, pick(ml[s][1]), L);
+    O[0] = fmaf(w, __uint_as_float(oa[s].x), O[0]);
+    O[1] = fmaf(w, __uint_as_float(oa[s].y), O[1]);
+    O[2] = fmaf(w, __uint_as_float(oa[s].z), O[2]);
+    O[3] = fmaf(w, __uint_as_float(oa[s].w), O[3]);
+    O[4] = fmaf(w, __uint_as_float(ob[s].x), O[4]);
+    O[5] = fmaf(w, __uint_as_float(ob[s].y), O[5]);
+    O[6] = fmaf(w, __uint_as_float(ob[s].z), O[6]);
+    O[7] = fmaf(w, __uint_as_float(ob[s].w), O[7]);
   }
-  if (t == 0) __hip_atomic_store(c.misc + MISC_HEAD + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float inv = 1.0f / L;
+  u32x4 out;
+  out.x = pack_bf2(O[0] * inv, O[1] * inv);
+  out.y = pack_bf2(O[2] * inv, O[3] * inv);
+  out.z = pack_bf2(O[4] * inv, O[5] * inv);
+  out.w = pack_bf2(O[6] * inv, O[7] * inv);
+  *reinterpret_cast<u32x4*>(att_lds + qh * HD + d0) = out;
 }
 
 __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   __shared__ float s_val[128];
   __shared__ AttnShared s_att;
+  __shared__ __attribute__((aligned(16))) uint16_t s_attv[H];
   __shared__ float s_best[NWAVE];
   __shared__ int s_bidx[NWAVE];
   __shared__ int s_last;
@@ -622,13 +673,19 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
 
       // ---- attention; the O-projection weights are prefetched meanwhile ----
       RowStream<2, 4> os;
-      const int nsplit = (c.n_rows + ATT_ROWS - 1) / ATT_ROWS;
+      int nsplit, rows;
+      attn_split(c.n_rows, nsplit, rows);
       const int nitems = NKV * nsplit;
+      float* part_l = c.part + (size_t)li * PART_LAYER_FLOATS;
       if (w < nitems) {
         os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)(R0 + wave) * (H * 2),
                  NWAVE * H * 2, wave_count(R0, R1));
         grid_wait(c.g);
-        for (int it = w; it < nitems; it += G) attn_item(c, li, it / nsplit, it % nsplit, nsplit, s_att);
+        for (int it = w; it < nitems; it += G) {
+          const int h = it / nsplit, sp = it % nsplit;
+          const int j0 = sp * rows, j1 = min(j0 + rows, c.n_rows);
+          attn_item(c, li, h, j0, j1, part_l + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, s_att);
+        }
         grid_arrive(c.g);
       } else {
         // no attention work: arrive at once without waiting on the QKV
@@ -640,9 +697,12 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
 
       // ---- O projection + residual -> h1 ----
       grid_wait(c.g);
+      attn_merge(part_l, nsplit, s_attv);
+      __syncthreads();
       {
         u32x4 xs[4];
-        load_x2048(c.buf(li, ACT_ATT), xs);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xs[i] = *reinterpret_cast<const u32x4*>(s_attv + i * 512 + lane * 8);
         const uint16_t* hprev = c.h_in(li);
         uint16_t* h1 = c.buf(li, ACT_H1);
         os.run([&](const u32x4(&wv)[4]) {
@@ -980,7 +1040,6 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   kp.rope_rows = w->rope_rows;
   kp.do_lm = do_lm ? 1 : 0;
   kp.flags = a->flags;
-  kp.max_split = max_split_for(a->s_max);
   kp.timeout_ticks = di.ticks_per_s * 2ull;   // 2 s per barrier wait
   kp.trace = static_cast<unsigned long long*>(a->trace);
 
