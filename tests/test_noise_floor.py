@@ -1,0 +1,64 @@
+"""Measures the floating-point noise floor that the GPU parity tolerances of
+tests/test_gpu_decode.py are set against (CPU only, seed-0 Llama-3.2-1B).
+
+From one identical state (128-token prefill, decode step at position 128) the
+oracle's logits move, with no change to the algorithm's bf16 rounding points,
+when only the accumulation precision changes (fp32 -> fp64), and they move when
+the softmax numerator keeps fp32 p instead of bf16(p). Both shifts exceed the
+north-star 2e-2 max-abs bound, which is why the full-model per-step bound is
+set from this floor; the test pins the floor so that choice stays justified.
+"""
+
+import torch
+
+from oracle.llama_ref import OracleLlama
+
+
+class _FP64Accumulate(OracleLlama):
+    """The oracle with fp64 accumulation and its bf16 rounding points kept."""
+
+    def __init__(self, sd):
+        super().__init__(sd, mode="exact")
+        self.mode = "mk"
+
+    def rnd(self, x):
+        return x.to(torch.bfloat16).to(self.dt)
+
+
+def test_full_model_step_noise_floor_exceeds_2e2(llama_1b_sd):
+    from mk_weights import random_token_ids
+    torch.set_num_threads(8)
+    ids = random_token_ids(129, seed=0)
+    o = OracleLlama(llama_1b_sd, mode="mk")
+    c = o.new_cache(1024)
+    o.forward(ids[:128], 0, c, want_logits=False)
+    a = o.forward(ids[128:], 128, [(k.clone(), v.clone()) for k, v in c])[0][0].double()
+    del o
+    o64 = _FP64Accumulate(llama_1b_sd)
+    b = o64.forward(ids[128:], 128, [(k.double(), v.double()) for k, v in c])[0][0]
+    d = (a - b).abs()
+    # same rounding points, different accumulation: above 2e-2, below the GPU test bounds
+    assert 0.02 < d.max().item() < 0.15
+    assert d.pow(2).mean().sqrt().item() < 0.03
+    assert int(a.argmax()) == int(b.argmax())
+
+
+def test_random_weight_greedy_agreement_floor(llama_1b_sd):
+    """Teacher-forced argmax agreement of the oracle with its fp64-accumulation
+    variant over the config-3 positions (384-token prompt, 640 more tokens):
+    about 93%, because random-init logits have tiny top-2 gaps. Where the gap is
+    >= 0.1 the two agree everywhere."""
+    from mk_weights import random_token_ids
+    torch.set_num_threads(8)
+    seq = torch.cat([random_token_ids(384, seed=0), random_token_ids(639, seed=7)])
+    o = OracleLlama(llama_1b_sd, mode="mk")
+    a = o.logits(o.forward(seq, 0, o.new_cache(1024), want_logits=False)[1][383:]).double()
+    del o
+    o64 = _FP64Accumulate(llama_1b_sd)
+    b = o64.logits(o64.forward(seq, 0, o64.new_cache(1024), want_logits=False)[1][383:])
+    del o64
+    same = a.argmax(-1) == b.argmax(-1)
+    top2 = b.topk(2, -1).values
+    decided = (top2[:, 0] - top2[:, 1]) >= 0.1
+    assert 0.85 < same.double().mean().item() < 0.99
+    assert same[decided].all()
