@@ -1,0 +1,204 @@
+"""Driver with the reference's CLI (main.py:34-105, 538-669) for this build.
+
+  python main.py --mode generate [--enable-nki] [--prompt-ids 1,2,3 | --prompt-len 384]
+                 [--max-new-tokens N] [--model-path random:0 | /path/to/hf_checkpoint]
+  python main.py --mode validate --enable-nki [...]
+  python main.py --mode benchmark --enable-nki [...]
+
+* generate: greedy generation with the megakernel model (the reference's
+  run_generation, main.py:360-375). Prompts are token ids (no tokenizer or
+  network here); ``--tokenizer-path`` decodes the output if a local tokenizer
+  is given.
+* validate: the megakernel model against the stock PyTorch path
+  (llama_baseline.StockLlama, fp32) on the same weights and token ids, with
+  teacher forcing after a divergence as in check_accuracy_logits
+  (main.py:274-357): per-step logit error and greedy agreement; the criteria
+  are those of tests/test_gpu_decode.py (bf16 noise floor, see there).
+* benchmark: e2e / context-encoding / token-generation latency percentiles and
+  throughput in the shape of NxDI's benchmark report (main.py:178-271),
+  written to benchmark_report.json.
+
+``--enable-nki`` selects the megakernel model (llama_with_megakernel), as in
+the reference (main.py:546-553); without it generate/benchmark run the stock
+path. ``--tp-degree`` must be 1 (llama_with_megakernel.py:147-150).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+
+BENCHMARK_REPORT_FILENAME = "benchmark_report.json"
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--mode", choices=["generate", "validate", "benchmark"], required=True)
+    ap.add_argument("--enable-nki", action="store_true")
+    ap.add_argument("--model-path", default="random:0")
+    ap.add_argument("--tokenizer-path", default=None)
+    ap.add_argument("--prompt-ids", default=None, help="comma-separated token ids")
+    ap.add_argument("--prompt-len", type=int, default=384, help="random prompt length (seed 0) if no ids")
+    ap.add_argument("--max-new-tokens", type=int, default=640)
+    ap.add_argument("--seq-len", type=int, default=1024)
+    ap.add_argument("--max-context-length", type=int, default=None)
+    ap.add_argument("--batch-size", type=int, default=1)
+    ap.add_argument("--tp-degree", type=int, default=1)
+    ap.add_argument("--top-k", type=int, default=1)
+    ap.add_argument("--num-runs", type=int, default=5)
+    ap.add_argument("--num-tokens-to-check", type=int, default=None)
+    return ap.parse_args(argv)
+
+
+def prompt_ids(args):
+    from mk_weights import random_token_ids
+    if args.prompt_ids:
+        return torch.tensor([int(x) for x in args.prompt_ids.split(",")], dtype=torch.int64)
+    return random_token_ids(args.prompt_len, seed=0)
+
+
+def prepare_inference(args):
+    from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
+    if args.top_k != 1:
+        raise SystemExit("only greedy decoding (top_k=1) is built")
+    nc = NeuronConfigLlamaMK(batch_size=args.batch_size, seq_len=args.seq_len,
+                             max_context_length=args.max_context_length or args.seq_len,
+                             tp_degree=args.tp_degree)
+    model = NeuronLlamaForCausalLM(args.model_path, LlamaInferenceConfig(nc))
+    t0 = time.monotonic()
+    model.compile()
+    model.load()
+    print(f"model ready in {time.monotonic() - t0:.1f}s (weights packed on the GPU)", flush=True)
+    return model
+
+
+def decode_text(args, ids):
+    if not args.tokenizer_path:
+        return None
+    from transformers import AutoTokenizer
+    tok = AutoTokenizer.from_pretrained(args.tokenizer_path, local_files_only=True)
+    return tok.decode(ids)
+
+
+def run_generation(args):
+    ids = prompt_ids(args)
+    if args.enable_nki:
+        model = prepare_inference(args)
+        out = model.generate(ids, args.max_new_tokens)
+    else:
+        from llama_baseline import StockLlama
+        from mk_weights import load_hf_checkpoint, synthetic_state_dict
+        sd = (synthetic_state_dict(int(args.model_path.split(":")[1] or 0)) if args.model_path.startswith("random:")
+              else load_hf_checkpoint(args.model_path))
+        base = StockLlama(sd, s_max=args.seq_len)
+        for p in range(len(ids) - 1):
+            base.step(int(ids[p]), p)
+        tok, out = int(ids[-1]), []
+        for t in range(args.max_new_tokens):
+            tok = int(base.step(tok, len(ids) - 1 + t).argmax())
+            out.append(tok)
+        out = torch.tensor(out)
+    print("Generated token ids:", out.tolist())
+    text = decode_text(args, out.tolist())
+    if text is not None:
+        print("Generated text:", text)
+    return out
+
+
+def run_accuracy_check(args) -> bool:
+    from llama_baseline import StockLlama
+    ids = prompt_ids(args)
+    model = prepare_inference(args)
+    toks, logits = model.generate(ids, args.max_new_tokens, return_logits=True)
+    n_check = args.num_tokens_to_check or args.max_new_tokens
+    base = StockLlama(model.state_dict_bf16, s_max=model.s_max)
+    seq = torch.cat([ids, toks.long()])
+    for p in range(len(ids) - 1):
+        base.step(int(seq[p]), p)
+    agree, decided, decided_ok, worst, worst_rms, first_div = 0, 0, 0, 0.0, 0.0, None
+    for t in range(n_check):
+        ref = base.step(int(seq[len(ids) - 1 + t]), len(ids) - 1 + t).cpu()
+        d = (logits[t] - ref).abs()
+        worst = max(worst, d.max().item())
+        worst_rms = max(worst_rms, d.pow(2).mean().sqrt().item())
+        same = int(ref.argmax()) == int(toks[t])
+        agree += same
+        if not same and first_div is None:
+            first_div = t
+        top2 = ref.topk(2).values
+        if float(top2[0] - top2[1]) >= 0.1:
+            decided += 1
+            decided_ok += same
+    rate = agree / n_check
+    rate_dec = decided_ok / max(decided, 1)
+    print(f"validate: {n_check} tokens, teacher-forced greedy agreement {rate * 100:.2f}% "
+          f"(where the baseline's top-2 gap >= 0.1: {rate_dec * 100:.2f}% of {decided}); "
+          f"first divergence at {first_div}; logits max|d| {worst:.3e}, worst per-step rms {worst_rms:.3e}")
+    return worst <= 0.2 and worst_rms <= 0.03 and rate_dec >= 0.99 and rate >= 0.90
+
+
+def benchmark_sampling(args):
+    ids = prompt_ids(args)
+    model = prepare_inference(args)
+    n_new = args.max_new_tokens
+    e2e, cte, tkg = [], [], []
+    for r in range(args.num_runs + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill(ids)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dec = model.launcher("decode")
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_new + 1)]
+        ev[0].record()
+        for i in range(n_new):
+            dec.launch()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if r == 0:
+            continue            # warm-up run
+        e2e.append((t2 - t0) * 1e3)
+        cte.append((t1 - t0) * 1e3)
+        tkg += [ev[i].elapsed_time(ev[i + 1]) for i in range(n_new)]
+
+    def rep(lat, tokens):
+        lat_s = sorted(lat)
+        pct = lambda q: lat_s[min(len(lat_s) - 1, int(q * len(lat_s)))]
+        return {"latency_ms_p50": pct(0.5), "latency_ms_p90": pct(0.9), "latency_ms_p99": pct(0.99),
+                "latency_ms_avg": statistics.mean(lat), "throughput": tokens / (statistics.mean(lat) / 1e3)}
+    report = {"e2e_model": rep(e2e, len(ids) + n_new),
+              "context_encoding_model": rep(cte, len(ids)),
+              "token_generation_model": rep(tkg, 1)}
+    print(json.dumps(report, indent=4))
+    Path(BENCHMARK_REPORT_FILENAME).write_text(json.dumps(report))
+    return report
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.mode == "generate":
+        run_generation(args)
+    elif args.mode == "validate":
+        if not args.enable_nki:
+            raise SystemExit("validate compares the megakernel model (--enable-nki) with the stock path")
+        ok = run_accuracy_check(args)
+        print(f"Validation {'passed' if ok else 'failed'}.")
+        return 0 if ok else 1
+    elif args.mode == "benchmark":
+        if not args.enable_nki:
+            raise SystemExit("benchmark measures the megakernel model (--enable-nki)")
+        benchmark_sampling(args)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
