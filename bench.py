@@ -34,6 +34,9 @@ sys.path.insert(0, str(REPO / "llama1b-megakernel_amd"))
 sys.path.insert(1, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (scaled by the plain-copy calibration); see profiles/mk_decode_kernel_c3_bs1.md
+TRAFFIC_JSON = REPO / "profiles" / "mk_decode_kernel_c3_bs1_traffic.json"
 PROMPT = 384
 S_MAX = 1024
 
@@ -83,7 +86,18 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=24)
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run 10 plain device copies of BYTES (HBM counter calibration for rocprofv3)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        src = torch.ones(args.copy_calibration // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": args.copy_calibration, "dispatches": 10}))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
@@ -137,6 +151,9 @@ def main():
     bytes_per_step = sum(step_bytes(16, [PROMPT + i], lm_head=True) for i in range(K)) / K
     achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
 
+    traffic = None
+    if TRAFFIC_JSON.exists():
+        traffic = int(json.loads(TRAFFIC_JSON.read_text())["traffic_bytes_per_step"])
     result = {
         "metric": "bs=1 decode tok/s + p50 step latency, Llama-3.2-1B ctx1024; HBM GB/s",
         "value": round(K / wall, 2),
@@ -156,7 +173,7 @@ def main():
                                f"KV cache, greedy steps at KV lengths {PROMPT}..{PROMPT + K - 1}",
                    "batch": 1, "prompt": PROMPT, "max_context_length": S_MAX, "n_layers": 16},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_step": int(bytes_per_step), "kernel": "mk_decode_kernel"},
         "cpu_baseline": None,
     }
