@@ -23,9 +23,9 @@
  *
  * Error convention: 0 on success, a negative MK_ERR_* code otherwise, with a
  * message from mk_last_error(). Arguments are validated before any HIP call.
- * Faults the device detects while running (a position out of range, a grid
- * barrier that timed out) set bits in the workspace; mk_read_device_error()
- * returns and clears them.
+ * Faults the device detects while running (a position out of range, a wait
+ * for another workgroup's results that timed out) set bits in the workspace;
+ * mk_read_device_error() returns and clears them.
  */
 #ifndef MK_H_
 #define MK_H_
@@ -50,7 +50,8 @@ extern "C" {
 
 /* Device-side error bits (mk_read_device_error). */
 #define MK_DEVERR_POS        0x1u  /* pos[b] < 0 or >= s_max or >= rope_rows: step skipped */
-#define MK_DEVERR_BARRIER    0x2u  /* a grid barrier exceeded its time limit */
+#define MK_DEVERR_SYNC       0x2u  /* a wait for another workgroup's results exceeded its time limit */
+#define MK_DEVERR_BARRIER    MK_DEVERR_SYNC   /* earlier name of the same bit */
 
 /* mk_step_args.flags */
 #define MK_FLAG_ADVANCE      0x1u  /* after the step: pos[b] += 1 (device side)   */
@@ -111,8 +112,8 @@ typedef struct mk_weights {
  *          norm and lm_head are skipped (the layer-stack seam of
  *          transformer_llama.py). next_token may alias tokens.
  *   workspace: device memory of at least mk_workspace_bytes(batch, s_max)
- *          bytes, 256-byte aligned, zeroed once with mk_workspace_init before
- *          first use; every step leaves it ready for the next.
+ *          bytes, 256-byte aligned, initialised once with mk_workspace_init
+ *          before first use; every step leaves it ready for the next.
  *   stream: hipStream_t (NULL = default stream).
  * Calls on one workspace must not overlap in time (same stream, or ordered).
  */
@@ -135,8 +136,12 @@ typedef struct mk_step_args {
     void *stream;
     /* Optional phase trace (NULL = off): device uint64 [grid][MK_TRACE_SLOTS].
      * Workgroup w records the device wall clock (mk_wall_clock_hz ticks/s) in
-     * slot 0 at start, 2k-1 when it arrives at grid barrier k (k = 1, 2, ...),
-     * 2k when its wait on barrier k returns, and MK_TRACE_SLOTS-1 at exit. */
+     * slot 0 at start, 2k-1 when it starts waiting for the input of hand-over
+     * k and 2k when that input has arrived, and MK_TRACE_SLOTS-1 at exit.
+     * Hand-over k = 5*i + j is phase j of run-layer i (1 QKV input, 2
+     * attention inputs, recorded by workgroups with attention work only, 3
+     * attention output, 4 h1, 5 gate/up output); k = 5*n_layers + 1 is the
+     * lm_head input. */
     void *trace;
 } mk_step_args;
 
@@ -152,7 +157,7 @@ long long mk_wall_clock_hz(int device);
 
 /* Workspace bytes for `batch` sequences with `s_max` cache rows; 0 if unsupported. */
 size_t mk_workspace_bytes(int32_t batch, int32_t s_max);
-/* Zero the workspace on `stream` with a fill kernel (graph-capturable). */
+/* Initialise the workspace on `stream` with a fill kernel (graph-capturable). */
 int mk_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 /* Synchronise `stream`, return the device error bits and clear them. */
 int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);

@@ -23,7 +23,8 @@ ERRORS = {
     -5: "MK_ERR_HIP", -6: "MK_ERR_DEVICE", -7: "MK_ERR_ALIGN",
 }
 MK_DEVERR_POS = 0x1
-MK_DEVERR_BARRIER = 0x2
+MK_DEVERR_SYNC = 0x2
+MK_DEVERR_BARRIER = MK_DEVERR_SYNC
 MK_FLAG_ADVANCE = 0x1
 
 HIDDEN, N_KV, HEAD_DIM, VOCAB, MAX_LAYERS = 2048, 8, 64, 128256, 16
