@@ -1,6 +1,6 @@
 // mk_decode.hip — Llama-3.2-1B token-generation megakernel for MI355X (gfx950).
 //
-// One cooperative launch runs a whole decode step: for every decoder layer
+// One kernel launch runs a whole decode step: for every decoder layer
 //   QKV  : RMSNorm(h) -> [Wq;Wk;Wv] GEMV -> RoPE -> q and the fresh K/V row,
 //          which is also written in place into the caches at row pos
 //                                                              (attention.py:69-245, 450-492)
@@ -16,7 +16,8 @@
 //
 // Design for CDNA4:
 //   * one 256-thread workgroup (4 wave64s, one per SIMD) per CU, grid = #CUs,
-//     launched cooperatively so all workgroups are co-resident;
+//     occupancy 1, so all workgroups are resident together (a plain launch on
+//     an idle device, or a cooperative launch on request);
 //   * no grid barriers. Phases hand their results over through per-layer
 //     exchange buffers that hold a sentinel (all-ones bits: a NaN the kernel
 //     never stores) until written. A producer stores its results with
@@ -1189,9 +1190,19 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   kp.trace = static_cast<unsigned long long*>(a->trace);
 
   void* args[] = {&kp};
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid),
-                                                  dim3(NT), args, 0, static_cast<hipStream_t>(a->stream));
-  if (e != hipSuccess) return fail(MK_ERR_HIP, "cooperative launch failed: %s", hipGetErrorString(e));
+  // One workgroup per CU with occupancy 1 (checked in device_info): on an
+  // otherwise idle device a plain launch makes every workgroup resident at
+  // once, and leaves ~20 us less between consecutive steps than a cooperative
+  // launch. MK_FLAG_COOPERATIVE asks for the guarantee. Every wait in the
+  // kernel is bounded, so a workgroup that is never scheduled shows up as
+  // MK_DEVERR_SYNC, not as a hang.
+  const hipStream_t st = static_cast<hipStream_t>(a->stream);
+  const hipError_t e =
+      (a->flags & MK_FLAG_COOPERATIVE)
+          ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args,
+                                       0, st)
+          : hipLaunchKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args, 0, st);
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return MK_OK;
 }
 

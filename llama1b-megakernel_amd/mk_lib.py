@@ -26,6 +26,7 @@ MK_DEVERR_POS = 0x1
 MK_DEVERR_SYNC = 0x2
 MK_DEVERR_BARRIER = MK_DEVERR_SYNC
 MK_FLAG_ADVANCE = 0x1
+MK_FLAG_COOPERATIVE = 0x2
 
 HIDDEN, N_KV, HEAD_DIM, VOCAB, MAX_LAYERS = 2048, 8, 64, 128256, 16
 

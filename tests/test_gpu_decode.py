@@ -228,3 +228,23 @@ def test_argmax_ties_resolve_to_lowest_index(model):
             assert int(lg.argmax()) == lo
     finally:
         emb[other] = saved
+
+
+def test_cooperative_launch_matches_plain_launch(model):
+    """MK_FLAG_COOPERATIVE only changes how the grid is launched: same state, same bits."""
+    import mk_lib
+    from mk_weights import random_token_ids
+    ids = random_token_ids(30, seed=9)
+    outs = []
+    for coop in (False, True):
+        model.prefill(ids)
+        flags = mk_lib.MK_FLAG_ADVANCE | (mk_lib.MK_FLAG_COOPERATIVE if coop else 0)
+        l = mk_lib.StepLauncher(model.weights, model.ws, model.k_caches, model.v_caches, model.pos,
+                                tokens=model.tokens, logits=model.logits, next_token=model.tokens, flags=flags)
+        l.launch()
+        torch.cuda.synchronize()
+        assert model.ws.read_device_error() == 0
+        outs.append((model.logits.clone(), int(model.tokens.item()), model.kv[:, :, 0, :, 29].clone()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert outs[0][1] == outs[1][1]
+    assert torch.equal(outs[0][2].view(torch.int16), outs[1][2].view(torch.int16))
