@@ -1,0 +1,498 @@
+// mk_common.h — device building blocks shared by the decode kernels of
+// libmk.so (mk_decode.hip: batch 1; mk_batch.hip: batches of 2..32).
+//
+// Numerics follow the reference's NKI kernels (nki_kernels/attention.py,
+// nki_kernels/mlp.py): bf16 storage, fp32 accumulation, bf16 rounding at the
+// same points. Hand-over waits poll sentinel-filled exchange buffers (see the
+// kernels' headers).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mk.h"
+
+namespace mk {
+
+constexpr int H = MK_HIDDEN;
+constexpr int NQ = MK_N_Q_HEADS;
+constexpr int NKV = MK_N_KV_HEADS;
+constexpr int HD = MK_HEAD_DIM;
+constexpr int GQA = NQ / NKV;
+constexpr int INTER = MK_INTER;
+constexpr int VOCAB = MK_VOCAB;
+constexpr int QKV_ROWS = MK_QKV_ROWS;
+constexpr int QKV_PAIRS = QKV_ROWS / 2;    // 1536 RoPE pairs
+constexpr int Q_PAIRS = NQ * HD / 2;       // 1024
+constexpr int K_PAIRS = NKV * HD / 2;      // 256
+constexpr int NT = 256;                    // threads per workgroup
+constexpr int NWAVE = NT / 64;
+constexpr int ATT_GROUP = 128;             // KV rows an attention item loads at once (4 rounds of 32)
+constexpr int PART_FLOATS = GQA * (HD + 2);  // per split: m[4], l[4], o[4][64]
+constexpr uint32_t OOB = 0x80000000u;      // buffer offset past every resource
+constexpr float EPS = 1e-5f;
+constexpr float SM_SCALE = 0.125f;         // 1/sqrt(64)
+
+constexpr size_t QKV_LAYER_BYTES = (size_t)QKV_ROWS * H * 2;
+constexpr size_t O_LAYER_BYTES = (size_t)H * H * 2;
+constexpr size_t GU_LAYER_BYTES = (size_t)2 * INTER * H * 2;
+constexpr size_t D_LAYER_BYTES = (size_t)H * INTER * 2;
+constexpr size_t EMBED_BYTES = (size_t)VOCAB * H * 2;
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even. Every NaN becomes the canonical
+// quiet NaN 0x7fc0, so the exchange sentinel 0xffff is never produced.
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float rbf(float f) { return __uint_as_float(f2bf(f) << 16); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+// fp32 for an exchange buffer: NaN canonicalised (never the 0xffffffff sentinel).
+__device__ __forceinline__ float canon(float f) { return f != f ? __uint_as_float(0x7fc00000u) : f; }
+
+// 8-element bf16 dot product accumulated in fp32 (v_dot2_f32_bf16). The
+// operands are bit-cast as whole 8-lane vectors and split with shufflevector:
+// bit-casting individual u32 components to bf16x2 miscompiles (all four
+// dot2 instructions end up reading the same register pair).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
+  const bf16x8_t A = __builtin_bit_cast(bf16x8_t, a), B = __builtin_bit_cast(bf16x8_t, b);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(A, A, 0, 1), __builtin_shufflevector(B, B, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(A, A, 2, 3), __builtin_shufflevector(B, B, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(A, A, 4, 5), __builtin_shufflevector(B, B, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(A, A, 6, 7), __builtin_shufflevector(B, B, 6, 7), acc, false);
+  return acc;
+}
+
+// Cross-lane moves. DPP (data-parallel primitives) read a neighbour lane's
+// register within the same instruction; readlane copies one lane to a scalar.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_val(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+constexpr int DPP_XOR1 = 0xb1;      // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4e;      // quad_perm [2,3,0,1]
+constexpr int DPP_ROR4 = 0x124;     // row_ror:4 (rotate within 16 lanes)
+constexpr int DPP_ROR8 = 0x128;     // row_ror:8
+
+// Sum over the 64 lanes, returned in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_ROR4>(v);
+  v += dpp<DPP_ROR8>(v);     // every lane now holds the sum of its 16-lane row
+  return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
+}
+
+constexpr int AUX_NT = 2, AUX_SC1 = 16;   // buffer-load cache policy bits (gfx950)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// Streaming 16-byte load (non-temporal); offsets >= the resource size read zero.
+__device__ __forceinline__ u32x4 ld_stream(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_NT);
+}
+__device__ __forceinline__ u32x4 ld16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+
+// Device-scope (sc1) accesses for data exchanged between workgroups within a
+// launch: the store writes through to the device coherence point, the load
+// never returns a line cached before that point was updated.
+__device__ __forceinline__ void st_dev(uint16_t* p, uint32_t bf_bits) {
+  __hip_atomic_store(p, (uint16_t)bf_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, canon(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u32x4 ld_dev16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_SC1);
+}
+__device__ __forceinline__ uint32_t ld_dev4(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX_SC1);
+}
+// Completion of this wave's outstanding memory operations (stores included).
+__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// Contiguous share [lo, hi) of `total` items for part `i` of `n`.
+__device__ __forceinline__ void share(int total, int n, int i, int& lo, int& hi) {
+  lo = (int)(((long long)total * i) / n);
+  hi = (int)(((long long)total * (i + 1)) / n);
+}
+
+// Sentinel tests. bf16 exchange data: any 16-bit lane equal to 0xffff.
+// fp32 exchange data: a whole word equal to 0xffffffff.
+__device__ __forceinline__ bool sent_bf16(uint32_t w) { return (w | 0xffff0000u) == 0xffffffffu || w >= 0xffff0000u; }
+__device__ __forceinline__ bool sent_bf16(u32x4 v) {
+  return sent_bf16(v.x) || sent_bf16(v.y) || sent_bf16(v.z) || sent_bf16(v.w);
+}
+
+// ---------------------------------------------------------------------------
+// Hand-over waits: bounded polls of exchange buffers
+// ---------------------------------------------------------------------------
+struct Sync {
+  uint32_t* err;
+  unsigned long long timeout;
+  unsigned long long* trace;   // this workgroup's MK_TRACE_SLOTS slots, or null
+};
+
+__device__ __forceinline__ void trace_mark(const Sync& s, int slot) {
+  if (s.trace && threadIdx.x == 0 && slot < MK_TRACE_SLOTS) s.trace[slot] = wall_clock64();
+}
+
+// True when a wait must give up: its time limit passed (the error bit is set
+// then) or another wait already gave up. Wave-uniform.
+__device__ __forceinline__ bool wait_expired(const Sync& s, unsigned long long t0, int it) {
+  if ((it & 15) == 0 &&
+      (__hip_atomic_load(s.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & MK_DEVERR_SYNC))
+    return true;
+  if (wall_clock64() - t0 > s.timeout) {
+    if (lane_id() == 0)
+      __hip_atomic_fetch_or(s.err, MK_DEVERR_SYNC, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  return false;
+}
+
+// Each lane polls N 16-byte pieces of bf16 exchange data (offsets into `r`;
+// OOB offsets read zero and count as ready) until the whole wave sees no
+// sentinel. A piece seen complete is not read again (its offset turns OOB),
+// so waiting consumers only re-read what is still missing. Called by full waves.
+template <int N>
+__device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_t (&off)[N], u32x4 (&v)[N]) {
+  const unsigned long long t0 = wall_clock64();
+  bool done[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) done[i] = false;
+  for (int it = 1;; ++it) {
+    u32x4 t[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = ld_dev16(r, done[i] ? OOB : off[i]);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (!done[i]) {
+        v[i] = t[i];
+        done[i] = !sent_bf16(t[i]);
+      }
+      ok = ok && done[i];
+    }
+    if (__all(ok)) return;
+    if (wait_expired(s, t0, it)) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Stage a bf16 vector of PER_WAVE*4 chunks of 512 elements into LDS: wave w
+// copies chunks w, w+4, ... Exchange buffers are polled; final data (the
+// embedding row, hidden_in) is read directly. The caller synchronises.
+template <int PER_WAVE>
+__device__ __forceinline__ void stage_vec(const Sync& s, const uint16_t* src, bool polled, uint16_t* lds) {
+  const int lane = lane_id(), wave = wave_id();
+  const rsrc_t r = make_rsrc(src, (size_t)PER_WAVE * NWAVE * 1024);
+  uint32_t off[PER_WAVE];
+  u32x4 v[PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) off[i] = (uint32_t)((wave + NWAVE * i) * 1024 + lane * 16);
+  if (polled) {
+    poll_bf16<PER_WAVE>(s, r, off, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) v[i] = ld16(r, off[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) *reinterpret_cast<u32x4*>(lds + (wave + NWAVE * i) * 512 + lane * 8) = v[i];
+}
+
+// Lane slice of a 2048-vector in LDS: elements i*512 + lane*8 .. +7.
+__device__ __forceinline__ void lds_x2048(const uint16_t* x, u32x4 (&xs)[4]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xs[i] = *reinterpret_cast<const u32x4*>(x + i * 512 + lane * 8);
+}
+
+// In-register RMSNorm of the wave's full 2048-vector copy:
+//   xn = bf16(x * rsqrt(mean(x^2) + eps))            (gamma folded into the weights)
+//   xn = bf16(g * bf16(x * rsqrt(mean(x^2) + eps)))  (final norm, HF LlamaRMSNorm)
+__device__ __forceinline__ void rmsnorm2048(u32x4 (&xs)[4], const uint16_t* gamma) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w[4] = {xs[i].x, xs[i].y, xs[i].z, xs[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf_lo(w[j]), b = bf_hi(w[j]);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss * (1.0f / H) + EPS);
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[4] = {xs[i].x, xs[i].y, xs[i].z, xs[i].w};
+    u32x4 gv = {0u, 0u, 0u, 0u};
+    if (gamma) gv = *reinterpret_cast<const u32x4*>(gamma + i * 512 + lane * 8);
+    const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a = rbf(bf_lo(w[j]) * inv), b = rbf(bf_hi(w[j]) * inv);
+      if (gamma) {
+        a = bf_lo(g[j]) * a;
+        b = bf_hi(g[j]) * b;
+      }
+      w[j] = pack_bf2(a, b);
+    }
+    xs[i] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+__device__ __forceinline__ float dot2048(const u32x4 (&wv)[4], const u32x4 (&xs)[4]) {
+  float a = dot8(wv[0], xs[0], 0.f);
+  float b = dot8(wv[1], xs[1], 0.f);
+  a = dot8(wv[2], xs[2], a);
+  b = dot8(wv[3], xs[3], b);
+  return a + b;
+}
+
+struct AttnShared {
+  float mx[NWAVE][GQA];
+  float sm[NWAVE][GQA];
+  float pv[NWAVE][8][GQA * 8];
+};
+
+__device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rrow, int d) {
+  // out[d]    = bf16(bf16(a*cos[d])    + bf16(-b*sin[d]))
+  // out[d+32] = bf16(bf16(b*cos[d+32]) + bf16( a*sin[d+32]))      (attention.py:160-174)
+  const float c0 = bf2f(rrow[d]), c1 = bf2f(rrow[d + 32]);
+  const float s0 = bf2f(rrow[64 + d]), s1 = bf2f(rrow[64 + d + 32]);
+  const float ra = rbf(rbf(a * c0) + rbf(-b * s0));
+  const float rb = rbf(rbf(b * c1) + rbf(a * s1));
+  return u32x4{f2bf(ra), f2bf(rb), 0u, 0u};
+}
+
+
+// One attention work item: one kv head of one sequence, cached KV rows
+// [j0, jc) plus, if `fresh`, the new row (from LDS), for the 4 q heads of the
+// group (GQA). kc_head / vc_head: the head's cache rows, bf16 [s_max][64];
+// q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
+// Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
+// of it; rows stream in groups of ATT_GROUP with an online softmax. Writes
+// the item's partial (m[4], l[4], o[4][64]) unnormalised, relative to m.
+__device__ __forceinline__ void attn_item(const uint16_t* kc_head, const uint16_t* vc_head, int s_max,
+                                          const uint16_t* q_lds, int j0, int jc, bool fresh, float* part,
+                                          AttnShared& sh) {
+  const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
+  const size_t head_bytes = (size_t)s_max * HD * 2;
+  const rsrc_t rk = make_rsrc(kc_head, head_bytes);
+  const rsrc_t rv = make_rsrc(vc_head, head_bytes);
+  u32x4 q[GQA];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(q_lds + g * HD + ch * 8);
+  float m_run[GQA], l_run[GQA], acc[GQA][8];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+  constexpr int R = ATT_GROUP / 32;
+  auto consume = [&](const u32x4(&kk)[R], const u32x4(&vv)[R], const bool(&valid)[R]) {
+    float sc[R][GQA];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int g = 0; g < GQA; ++g) {
+        float x = dot8(kk[r], q[g], 0.f);
+        x += __shfl_xor(x, 1, 64);
+        x += __shfl_xor(x, 2, 64);
+        x += __shfl_xor(x, 4, 64);
+        sc[r][g] = valid[r] ? x * SM_SCALE : -INFINITY;
+      }
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      float mn = m_run[g];
+#pragma unroll
+      for (int r = 0; r < R; ++r) mn = fmaxf(mn, sc[r][g]);
+      const float keep = mn == -INFINITY ? 1.f : __expf(m_run[g] - mn);
+      l_run[g] *= keep;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float pr = valid[r] ? __expf(sc[r][g] - mn) : 0.f;
+        l_run[g] += pr;
+        const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[g][2 * e] = fmaf(pr, bf_lo(w4[e]), acc[g][2 * e]);
+          acc[g][2 * e + 1] = fmaf(pr, bf_hi(w4[e]), acc[g][2 * e + 1]);
+        }
+      }
+      m_run[g] = mn;
+    }
+  };
+  // cached rows in groups of ATT_GROUP, the next group's loads in flight while one is consumed
+  auto load_group = [&](int base, u32x4(&kk)[R], u32x4(&vv)[R], bool(&valid)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = base + 32 * r + rl;
+      valid[r] = j < jc;
+      const uint32_t off = valid[r] ? (uint32_t)(j * HD + ch * 8) * 2u : OOB;
+      kk[r] = ld_stream(rk, off);
+      vv[r] = ld_stream(rv, off);
+    }
+  };
+  const int ngroups = jc > j0 ? (jc - j0 + ATT_GROUP - 1) / ATT_GROUP : 0;
+  u32x4 kA[R], vA[R];
+  bool validA[R];
+  if (ngroups > 0) load_group(j0, kA, vA, validA);
+  for (int gi = 0; gi < ngroups; ++gi) {
+    u32x4 kB[R], vB[R];
+    bool validB[R];
+    const bool more = gi + 1 < ngroups;
+    if (more) load_group(j0 + (gi + 1) * ATT_GROUP, kB, vB, validB);
+    consume(kA, vA, validA);
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        kA[r] = kB[r];
+        vA[r] = vB[r];
+        validA[r] = validB[r];
+      }
+    }
+  }
+  if (fresh) {   // the new row: row-lane 0 of the first round
+    u32x4 kk[R], vv[R];
+    bool valid[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      valid[r] = r == 0 && rl == 0;
+      kk[r] = valid[r] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + ch * 8) : u32x4{0u, 0u, 0u, 0u};
+      vv[r] = valid[r] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + HD + ch * 8) : u32x4{0u, 0u, 0u, 0u};
+    }
+    consume(kk, vv, valid);
+  }
+  // merge the 32 row-lanes of the item: max, rescale, sum (lanes of one row agree)
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    float m = m_run[g];
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane == 0) sh.mx[wave][g] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
+    const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
+    float l = l_run[g] * f;
+    l += __shfl_xor(l, 8, 64);
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (lane == 0) sh.sm[wave][g] = l;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[g][e] * f;
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[g][e] = v;
+    }
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int g = 0; g < GQA; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sh.pv[wave][ch][g * 8 + e] = acc[g][e];
+  }
+  __syncthreads();
+  {
+    const int g = t >> 6, d = t & 63;
+    float o = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < NWAVE; ++wv) o += sh.pv[wv][d >> 3][g * 8 + (d & 7)];
+    st_dev(part + 2 * GQA + g * HD + d, o);
+    if (t < GQA) {
+      st_dev(part + t, fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t])));
+      st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
+    }
+  }
+  __syncthreads();   // LDS reuse by a following item
+}
+
+// Split of [0, n_rows) into nsplit items of `rows` rows (a multiple of 32):
+// one item per min_rows rows, at most max_split items.
+__device__ __forceinline__ void attn_split(int n_rows, int max_split, int min_rows, int& nsplit, int& rows) {
+  int ns = (n_rows + min_rows - 1) / min_rows;
+  ns = ns < max_split ? ns : max_split;
+  rows = ((n_rows + ns - 1) / ns + 31) / 32 * 32;
+  nsplit = (n_rows + rows - 1) / rows;
+}
+
+// Merge the nsplit partials of one kv head (polled; split s at
+// part_head + s * PART_FLOATS) into the bf16 attention output of its 4 q heads:
+//   att = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s   (then cast to bf16)
+// Thread t produces q head (t >> 6) of the group, dim t & 63, at att[(t >> 6) * 64 + (t & 63)].
+constexpr int ATT_MERGE_MAX = 8;   // splits a merge reads at most
+__device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* part_head, int nsplit, uint16_t* att) {
+  const int t = threadIdx.x, g = t >> 6, d = t & 63;
+  const rsrc_t r = make_rsrc(part_head, (size_t)nsplit * PART_FLOATS * 4);
+  uint32_t m[ATT_MERGE_MAX], l[ATT_MERGE_MAX], o[ATT_MERGE_MAX];
+  const unsigned long long t0 = wall_clock64();
+  for (int it = 1;; ++it) {
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < ATT_MERGE_MAX; ++s) {   // splits >= nsplit read zero (out of range)
+      const uint32_t base = (uint32_t)(s * PART_FLOATS) * 4u;
+      m[s] = ld_dev4(r, base + (uint32_t)g * 4u);
+      l[s] = ld_dev4(r, base + (uint32_t)(GQA + g) * 4u);
+      o[s] = ld_dev4(r, base + (uint32_t)(2 * GQA + g * HD + d) * 4u);
+    }
+#pragma unroll
+    for (int s = 0; s < ATT_MERGE_MAX; ++s) ok = ok && m[s] != 0xffffffffu && l[s] != 0xffffffffu && o[s] != 0xffffffffu;
+    if (__all(ok)) break;
+    if (wait_expired(sy, t0, it)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < ATT_MERGE_MAX; ++s)
+    if (s < nsplit) M = fmaxf(M, __uint_as_float(m[s]));
+  float O = 0.f, Lsum = 0.f;
+#pragma unroll
+  for (int s = 0; s < ATT_MERGE_MAX; ++s) {
+    const float wgt = s < nsplit ? __expf(__uint_as_float(m[s]) - M) : 0.f;
+    Lsum = fmaf(wgt, __uint_as_float(l[s]), Lsum);
+    O = fmaf(wgt, __uint_as_float(o[s]), O);
+  }
+  const uint32_t mine = f2bf(O / Lsum);
+  const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine, DPP_XOR1, 0xf, 0xf, false);
+  if ((d & 1) == 0) st_dev(reinterpret_cast<uint32_t*>(att + g * HD + d), mine | (next << 16));
+}
+
+}  // namespace mk
