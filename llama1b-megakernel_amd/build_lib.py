@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parent
-SOURCES = [HERE / "csrc" / "mk_decode.hip"]
+SOURCES = [HERE / "csrc" / "mk_decode.hip", HERE / "csrc" / "mk_batch.hip"]
 LIB = HERE / "libmk.so"
 
 HIPCC_FLAGS = [

@@ -1,0 +1,78 @@
+// mk_batch.h — internal interface between the C ABI (mk_decode.hip) and the
+// batched decode kernel (mk_batch.hip). Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mk.h"
+
+namespace mk {
+
+constexpr int BATCH_MAX = 32;       // sequences one batched step serves
+constexpr int BATT_MAX_SPLIT = 16;  // KV-length splits per (sequence, kv head)
+
+// Workspace of a batched step (max batch M >= 2), bytes:
+//   [0, 256)          control words (exit counter, error bits, epoch), as for batch 1
+//   256 + 256*b       u64 argmax key of sequence b (one 256-byte line each)
+//   BWS_CNT0(M) + set*bws_cnt_set(M)     arrival counters of one launch (two sets,
+//                     alternating by epoch; each launch zeroes the other set):
+//     hand-over counters [MK_MAX_LAYERS][5 hand-overs][8 sub-counters], one 128-byte line each
+//     attention-split counters u32 [MK_MAX_LAYERS][M][8 kv heads]
+constexpr size_t BWS_KEY0 = 256;
+constexpr size_t BWS_KEY_STRIDE = 256;
+constexpr int N_HANDOVER = 5;   // per layer: qkv, att, h1, act, h2
+constexpr int N_SUB = 8;        // sub-counters per hand-over (arrivals spread over 8 lines)
+constexpr size_t CNT_LINE = 128;
+constexpr size_t HCNT_BYTES = (size_t)MK_MAX_LAYERS * N_HANDOVER * N_SUB * CNT_LINE;
+__host__ __device__ inline size_t bws_cnt0(int M) { return BWS_KEY0 + (size_t)M * BWS_KEY_STRIDE; }
+__host__ __device__ inline size_t bws_cnt_set(int M) {
+  return HCNT_BYTES + (size_t)MK_MAX_LAYERS * M * MK_N_KV_HEADS * 4;
+}
+__host__ __device__ inline size_t batch_ws_bytes(int M) { return bws_cnt0(M) + 2 * bws_cnt_set(M); }
+// Largest batch a workspace of `bytes` serves with the batched layout (< 2: batch-1 layout).
+inline int batch_of_ws_bytes(size_t bytes) {
+  if (bytes < batch_ws_bytes(2)) return 1;
+  int m = 2;
+  while (m < BATCH_MAX && batch_ws_bytes(m + 1) <= bytes) ++m;
+  return m;
+}
+
+// Exchange area of a batched step for up to M sequences (bytes), ordinary
+// device memory. Per layer (each part on a 256-byte boundary):
+//   qkv  bf16 [M][3072]   q | fresh k | fresh v of each token
+//   att  bf16 [M][2048]   merged attention output
+//   h1   bf16 [M][2048]   h + attn
+//   act  bf16 [M][8192]   silu(gate) * up
+//   h2   bf16 [M][2048]   layer output
+// and, after all layers, the attention partials
+//   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)].
+// Every buffer is written once per launch and read only after its arrival
+// counter is complete.
+struct BatchLayout {
+  size_t qkv, att, h1, act, h2, layer;   // within a layer
+  size_t part_base, part_layer, total;
+  static constexpr size_t r256(size_t x) { return (x + 255) / 256 * 256; }
+  void init(int M) {
+    qkv = 0;
+    att = r256(qkv + (size_t)M * MK_QKV_ROWS * 2);
+    h1 = r256(att + (size_t)M * MK_HIDDEN * 2);
+    act = r256(h1 + (size_t)M * MK_HIDDEN * 2);
+    h2 = r256(act + (size_t)M * MK_INTER * 2);
+    layer = r256(h2 + (size_t)M * MK_HIDDEN * 2);
+    part_base = (size_t)MK_MAX_LAYERS * layer;
+    part_layer = r256((size_t)M * MK_N_KV_HEADS * BATT_MAX_SPLIT * 4 * (MK_HEAD_DIM + 2) * 4);
+    total = part_base + (size_t)MK_MAX_LAYERS * part_layer;
+  }
+};
+
+// Grid check of the batched kernel on a device (occupancy 1 per CU); MK_OK or an MK_ERR code.
+int batch_device_check(int dev, char* msg, size_t msg_len);
+
+// Enqueue one batched step (arguments already validated by mk_decode_step):
+// xch = exchange area of BatchLayout(max_batch).total bytes.
+hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, int max_batch, int grid,
+                        unsigned long long timeout_ticks);
+
+}  // namespace mk

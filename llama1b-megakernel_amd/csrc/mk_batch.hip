@@ -1,0 +1,875 @@
+// mk_batch.hip — batched decode step of libmk.so for MI355X (gfx950): one
+// persistent launch advances up to 32 independent sequences by one token.
+//
+// Same phases as the batch-1 kernel (mk_decode.hip) — per layer QKV (RMSNorm,
+// projection, RoPE, K/V scatter at each sequence's own position), split-K GQA
+// attention over each sequence's own KV length, O projection + residual,
+// RMSNorm + gate/up + SwiGLU, down projection + residual; then final norm,
+// tied lm_head and a greedy argmax per sequence — with these differences:
+//
+//   * projections are bf16 MFMA GEMMs (v_mfma_f32_16x16x32_bf16, fp32
+//     accumulation): the tokens of the batch are the M dimension (one 16-row
+//     tile for up to 16 sequences, two for up to 32), 16 weight rows the N
+//     dimension. Each lane streams its B operand straight from HBM: 16 bytes
+//     of one weight row per k-step (row n0 + lane%16, columns k + (lane/16)*8),
+//     so every weight byte is loaded once per step, as at batch 1;
+//   * phases with one 16-row tile per workgroup (QKV, O, down) split K over
+//     the 4 waves and sum the 4 partial tiles through LDS in a fixed order;
+//     phases with many tiles per workgroup (gate/up, lm_head) give each wave
+//     whole tiles;
+//   * the A operand (activations) comes from LDS where the input is normalised
+//     (QKV, gate/up, lm_head: the staged [tokens][2048] matrix), or straight
+//     from the exchange buffer in MFMA layout (O, down);
+//   * hand-overs use arrival counters instead of sentinel data: every
+//     activation matrix is read by every workgroup, so consumers read it with
+//     ordinary loads that the XCD's L2 serves to its 32 CUs after the first
+//     fetch. A producer workgroup stores its results (device scope), waits
+//     for the stores to complete and adds one to its sub-counter (8 per
+//     hand-over, on separate lines, so arrivals do not queue on one line); a
+//     consumer polls the 8 sub-counters, then reads. A buffer is written once
+//     per launch and read only after its counter is complete, and every
+//     launch starts with invalidated caches, so no cached copy is stale;
+//   * staged inputs go straight from memory into LDS (buffer loads to LDS),
+//     leaving the registers to the weight stream;
+//   * attention work items are (sequence, kv head, KV split), sized from all
+//     sequences' lengths so the grid gets balanced work; the partials of a
+//     (sequence, kv head) are merged by whichever workgroup finishes its last
+//     split (an arrival counter), so no workgroup waits for another's
+//     attention work.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "mk.h"
+#include "mk_batch.h"
+#include "mk_common.h"
+
+namespace {
+
+using namespace mk;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int XS = H + 8;      // LDS row stride (bf16) of a staged activation matrix (+16 B against bank conflicts)
+constexpr int RES_MAX = 64;    // residual columns per workgroup kept in LDS (H / 32 at the smallest grid)
+constexpr int KQ = H / NWAVE;  // 512: the K range of one wave in the split-K phases over H
+constexpr int KS = 16;         // k-steps (of 32 columns) in a weight unit of the LDS-operand phases
+constexpr int DKS = 8;         // k-steps in a unit of the down projection (A operand in registers too)
+constexpr int ATT_MIN_ROWS = 128;
+constexpr int B_MIN_GRID = 32;
+constexpr int C_EXIT = 0, C_ERR = 1, C_EPOCH = 2;   // control words (shared with the batch-1 layout)
+constexpr int HO_QKV = 0, HO_ATT = 1, HO_H1 = 2, HO_ACT = 3, HO_H2 = 4;   // hand-overs of a layer
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+struct BParams {
+  const uint16_t* w_qkv;
+  const uint16_t* w_o;
+  const uint16_t* w_gu;
+  const uint16_t* w_d;
+  const uint16_t* embed;
+  const uint16_t* g_final;
+  const uint16_t* rope;
+  uint16_t* kc[MK_MAX_LAYERS];
+  uint16_t* vc[MK_MAX_LAYERS];
+  const int32_t* tokens;
+  const uint16_t* hidden_in;
+  int32_t* pos;
+  uint16_t* hidden_out;
+  float* logits;
+  int32_t* next_token;
+  uint8_t* ws;
+  uint8_t* xch;
+  BatchLayout lay;
+  int batch;
+  int max_batch;
+  int first_layer;
+  int n_layers;
+  int s_max;
+  int rope_rows;
+  int do_lm;
+  uint32_t flags;
+  unsigned long long timeout_ticks;
+  unsigned long long* trace;
+};
+
+template <int MT>
+struct BLds {
+  __attribute__((aligned(16))) uint16_t xn[16 * MT][XS];        // staged activation (normalised in place)
+  __attribute__((aligned(16))) uint16_t res[16 * MT][RES_MAX];  // raw columns [R0, R1) of the staged input
+  f32x4 red[NWAVE][MT][64];                                     // split-K partial tiles
+  __attribute__((aligned(16))) uint16_t q[GQA * HD + 2 * HD];    // attention: 4 q heads | fresh k | fresh v
+  AttnShared att;
+  unsigned long long key[NWAVE][16 * MT];
+  int pos[BATCH_MAX];
+  int tok[BATCH_MAX];
+  int ns[BATCH_MAX];
+  int rows[BATCH_MAX];
+  int cum[BATCH_MAX + 1];
+  int flag;
+};
+
+struct BCtx {
+  const BParams* p;
+  Sync s;
+  int G, w, B;
+  uint8_t* hcnt;    // this launch's hand-over counters [layer][5][8 lines]
+  uint32_t* acnt;   // this launch's attention-split counters [layer][M][8]
+  __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
+    return reinterpret_cast<uint16_t*>(p->xch + (size_t)li * p->lay.layer + off);
+  }
+  __device__ __forceinline__ float* part(int li, int b, int h, int sp) const {
+    return reinterpret_cast<float*>(p->xch + p->lay.part_base + (size_t)li * p->lay.part_layer) +
+           ((size_t)(b * NKV + h) * BATT_MAX_SPLIT + sp) * PART_FLOATS;
+  }
+  __device__ __forceinline__ uint32_t* ho(int li, int k) const {
+    return reinterpret_cast<uint32_t*>(hcnt + ((size_t)li * N_HANDOVER + k) * N_SUB * CNT_LINE);
+  }
+};
+
+__device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
+
+// ---------------------------------------------------------------------------
+// Hand-overs
+// ---------------------------------------------------------------------------
+
+// The workgroup's results of a phase are complete: every thread's stores
+// have finished, then one arrival is added to sub-counter `sub` of the hand-over.
+__device__ __forceinline__ void arrive(uint32_t* ho, int sub) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ho) + (size_t)sub * CNT_LINE), 1u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait (one full wave) until sub-counter j of a hand-over holds per + (j < extra) arrivals.
+__device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho, int per, int extra) {
+  const int lane = lane_id();
+  const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
+  const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
+  const uint32_t target = lane < N_SUB ? (uint32_t)(per + (lane < extra ? 1 : 0)) : 0u;
+  const unsigned long long t0 = wall_clock64();
+  for (int it = 1;; ++it) {
+    const uint32_t v = ld_dev4(r, off);
+    if (__all(v >= target)) return;
+    if (wait_expired(sy, t0, it)) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+// A hand-over produced by every workgroup of the grid (workgroup w adds to sub-counter w % 8).
+__device__ __forceinline__ void wait_grid(const BCtx& c, int li, int k) {
+  wait_handover(c.s, c.ho(li, k), c.G / N_SUB, c.G % N_SUB);
+}
+
+// ---------------------------------------------------------------------------
+// Operand movement
+// ---------------------------------------------------------------------------
+
+// The B-operand pieces of one weight unit of N k-steps: lane l holds row
+// row + l%16 (rows >= row_end read zero without a memory access) at columns
+// k0 + s*32 + (l/16)*8 .. +7 for k-step s.
+template <int N>
+__device__ __forceinline__ void load_w(rsrc_t r, int row, int row_end, uint32_t row_bytes, int k0, u32x4 (&wv)[N]) {
+  const int lane = lane_id();
+  const int n = row + (lane & 15);
+  const uint32_t o = n < row_end ? (uint32_t)n * row_bytes + (uint32_t)(k0 + (lane >> 4) * 8) * 2u : OOB;
+#pragma unroll
+  for (int s = 0; s < N; ++s) wv[s] = ld_stream(r, o + (uint32_t)s * 64u);
+}
+
+// The A-operand pieces of N k-steps read straight from an exchange matrix
+// [B][row_elems] (ordinary loads): a[mt*N + s] = token mt*16 + lane%16,
+// columns k0 + s*32 + (lane/16)*8 .. +7; tokens >= B read zero.
+template <int MT, int N>
+__device__ __forceinline__ void load_a(rsrc_t r, int B, int row_elems, int k0, u32x4 (&a)[MT * N]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + (lane & 15);
+    const uint32_t o = m < B ? (uint32_t)m * (uint32_t)(row_elems * 2) + (uint32_t)(k0 + (lane >> 4) * 8) * 2u : OOB;
+#pragma unroll
+    for (int s = 0; s < N; ++s) a[mt * N + s] = ld16(r, o + (uint32_t)s * 64u);
+  }
+}
+
+// Stage the [B][2048] bf16 input of a phase into LDS with buffer loads to LDS
+// (rows >= B zero), then RMS-normalise every row in place, keeping the raw
+// columns [r0, r1) in L.res:
+//   xn = bf16(x * rsqrt(mean(x^2) + eps))               (gamma folded into the weights)
+//   xn = bf16(g * bf16(x * rsqrt(mean(x^2) + eps)))     (final norm, gamma g)
+// src: an exchange buffer or hidden_in (row b at b*4096 bytes), or the
+// embedding table (gather: row of token L.tok[b]).
+template <int MT>
+__device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gather, const uint16_t* gamma, int r0,
+                                           int r1, BLds<MT>& L) {
+  const int wave = wave_id(), lane = lane_id();
+  // 1 KiB quarters of rows: wave w copies quarters w, w+4, ... (16*MT each)
+#pragma unroll
+  for (int j = 0; j < 16 * MT; ++j) {
+    const int qi = j * NWAVE + wave, m = qi >> 2, qq = qi & 3;
+    const uint32_t row = gather ? (uint32_t)L.tok[m < BATCH_MAX ? m : 0] : (uint32_t)m;
+    const uint32_t off = m < c.B ? row * (uint32_t)(H * 2) + (uint32_t)(qq * 1024 + lane * 16) : OOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr_t)&L.xn[m][qq * 512], 16, off, 0, 0, 0);
+  }
+  wait_mem();
+  __syncthreads();
+  // RMS per row: 8 threads (one lane octet) per row, chunks q8 + 8i (i < 32) of 8 elements
+  const int m = threadIdx.x >> 3, q8 = threadIdx.x & 7;
+  const bool rowv = m < 16 * MT;
+  float ss = 0.f;
+  if (rowv) {
+    for (int i = 0; i < 32; ++i) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][(q8 + 8 * i) * 8]);
+      const uint32_t e[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a = bf_lo(e[k]), b = bf_hi(e[k]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  }
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  ss += __shfl_xor(ss, 4, 64);
+  const float inv = rsqrtf(ss * (1.0f / H) + EPS);
+  if (rowv) {
+    for (int i = 0; i < 32; ++i) {
+      const int col = (q8 + 8 * i) * 8;
+      u32x4* px = reinterpret_cast<u32x4*>(&L.xn[m][col]);
+      const u32x4 x = *px;
+      uint32_t e[4] = {x.x, x.y, x.z, x.w};
+      if (col + 8 > r0 && col < r1) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (col + q >= r0 && col + q < r1) L.res[m][col + q - r0] = (uint16_t)(e[q >> 1] >> (16 * (q & 1)));
+      }
+      u32x4 gv = {0u, 0u, 0u, 0u};
+      if (gamma) gv = *reinterpret_cast<const u32x4*>(gamma + col);
+      const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float a = rbf(bf_lo(e[k]) * inv), b = rbf(bf_hi(e[k]) * inv);
+        if (gamma) {
+          a = bf_lo(g[k]) * a;
+          b = bf_hi(g[k]) * b;
+        }
+        e[k] = pack_bf2(a, b);
+      }
+      *px = u32x4{e[0], e[1], e[2], e[3]};
+    }
+  }
+  __syncthreads();
+}
+
+// One unit of MFMAs: KS k-steps from column k0, A from the staged LDS matrix.
+template <int MT>
+__device__ __forceinline__ void mma_lds(const BLds<MT>& L, int k0, const u32x4 (&wv)[KS], f32x4 (&acc)[MT]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(&L.xn[mt * 16 + (lane & 15)][k0 + s * 32 + (lane >> 4) * 8]);
+      acc[mt] = mfma16(a, wv[s], acc[mt]);
+    }
+}
+// One unit of MFMAs with the A operand in registers (a[mt*N + s]).
+template <int MT, int N>
+__device__ __forceinline__ void mma_reg(const u32x4 (&a)[MT * N], const u32x4 (&wv)[N], f32x4 (&acc)[MT]) {
+#pragma unroll
+  for (int s = 0; s < N; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16(a[mt * N + s], wv[s], acc[mt]);
+}
+
+// Sum of the 4 waves' partial tiles (fixed order); waves < MT receive the
+// full tile of token tile `wave`. The caller synchronises before L.red is reused.
+template <int MT>
+__device__ __forceinline__ f32x4 reduce_waves(const f32x4 (&acc)[MT], BLds<MT>& L) {
+  const int wave = wave_id(), lane = lane_id();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) L.red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  f32x4 d = {0.f, 0.f, 0.f, 0.f};
+  if (wave < MT) {
+    d = L.red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < NWAVE; ++w) d += L.red[w][wave][lane];
+  }
+  return d;
+}
+
+// ---------------------------------------------------------------------------
+// Phases
+// ---------------------------------------------------------------------------
+
+// QKV: RMSNorm of the layer input, [Wq;Wk;Wv] GEMM (split-K over the waves),
+// RoPE at each sequence's position; q and the fresh K/V rows to the exchange
+// buffer, K/V also into the caches at row pos[b] of sequence b.
+template <int MT>
+__device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  int P0, P1, R0, R1;
+  share(QKV_PAIRS, c.G, c.w, P0, P1);
+  share(H, c.G, c.w, R0, R1);
+  const int row0 = 2 * P0, row_end = 2 * P1, ntile = (row_end - row0 + 15) / 16;
+  const rsrc_t rw = make_rsrc(p.w_qkv + (size_t)l * QKV_ROWS * H, QKV_LAYER_BYTES);
+  u32x4 wv[KS];
+  load_w<KS>(rw, ntile > 0 ? row0 : row_end, row_end, H * 2, wave * KQ, wv);
+  trace_mark(c.s, 2 * xk(li, 1) - 1);
+  if (li > 0) {
+    wait_grid(c, li - 1, HO_H2);
+    stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+  } else if (p.hidden_in) {
+    stage_norm<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+  } else {
+    stage_norm<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, nullptr, R0, R1, L);
+  }
+  trace_mark(c.s, 2 * xk(li, 1));
+  uint16_t* xq = c.xb(li, p.lay.qkv);
+  for (int tt = 0; tt < ntile; ++tt) {
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mma_lds<MT>(L, wave * KQ, wv, acc);
+    if (tt + 1 < ntile) load_w<KS>(rw, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
+    const f32x4 d = reduce_waves<MT>(acc, L);
+    if (wave < MT) {
+      const int row = row0 + tt * 16 + (lane & 15);
+      const bool rv = row < row_end;
+      const int pr = row >> 1, dd = pr & 31, hi = row & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float mine = rbf(d[i]);
+        const float other = dpp<DPP_XOR1>(mine);   // the pair partner (row ^ 1)
+        const int m = wave * 16 + (lane >> 4) * 4 + i;
+        if (!rv || m >= c.B) continue;
+        const float a = hi ? other : mine, b = hi ? mine : other;   // elements d, d+32
+        const int ps = L.pos[m];
+        uint32_t outv;
+        if (pr < Q_PAIRS + K_PAIRS) {
+          const u32x4 o = rope_pair(a, b, p.rope + (size_t)ps * (2 * HD), dd);
+          outv = hi ? o.y : o.x;
+        } else {
+          outv = f2bf(mine);
+        }
+        int col;
+        if (pr < Q_PAIRS) {
+          col = (pr >> 5) * HD + dd + 32 * hi;
+        } else {
+          const bool is_k = pr < Q_PAIRS + K_PAIRS;
+          const int kh = (pr - Q_PAIRS - (is_k ? 0 : K_PAIRS)) >> 5;
+          col = NQ * HD + (is_k ? 0 : NKV * HD) + kh * HD + dd + 32 * hi;
+          // the cache row is read only by later launches: a plain store
+          uint16_t* crow = (is_k ? p.kc[li] : p.vc[li]) + ((size_t)(m * NKV + kh) * p.s_max + ps) * HD + dd + 32 * hi;
+          *crow = (uint16_t)outv;
+        }
+        st_dev(xq + (size_t)m * QKV_ROWS + col, outv);
+      }
+    }
+    __syncthreads();   // L.red reuse
+  }
+  arrive(c.ho(li, HO_QKV), c.w % N_SUB);
+}
+
+// Attention: the workgroup's items (sequence, kv head, split); the last split
+// of a (sequence, kv head) to arrive merges its partials.
+template <int MT>
+__device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int lane = lane_id(), t = threadIdx.x;
+  const int nitems = L.cum[c.B];
+  const rsrc_t rq = make_rsrc(c.xb(li, p.lay.qkv), (size_t)c.B * QKV_ROWS * 2);
+  bool waited = false;
+  for (int it = c.w; it < nitems; it += c.G) {
+    int b = 0;
+    while (L.cum[b + 1] <= it) ++b;
+    const int nsb = L.ns[b], rr = it - L.cum[b], h = rr / nsb, sp = rr % nsb;
+    const int ps = L.pos[b], rows = L.rows[b];
+    const int j0 = sp * rows, j1 = min(j0 + rows, ps + 1);
+    const bool fresh = ps >= j0 && ps < j1;
+    if (wave_id() == 0) {
+      if (!waited) {
+        trace_mark(c.s, 2 * xk(li, 2) - 1);
+        wait_grid(c, li, HO_QKV);
+        trace_mark(c.s, 2 * xk(li, 2));
+      }
+      // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
+      const uint32_t base = (uint32_t)b * (QKV_ROWS * 2);
+      const uint32_t off = lane < 32 ? base + (uint32_t)(h * GQA * HD * 2 + lane * 16)
+                         : lane < 40 ? (fresh ? base + (uint32_t)((NQ * HD + h * HD) * 2 + (lane - 32) * 16) : OOB)
+                         : lane < 48 ? (fresh ? base + (uint32_t)((NQ * HD + NKV * HD + h * HD) * 2 + (lane - 40) * 16) : OOB)
+                                     : OOB;
+      const u32x4 v = ld16(rq, off);
+      if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v;
+    }
+    waited = true;
+    __syncthreads();
+    const size_t head = (size_t)(b * NKV + h) * p.s_max * HD;
+    attn_item(p.kc[li] + head, p.vc[li] + head, p.s_max, L.q, j0, min(j1, ps), fresh, c.part(li, b, h, sp), L.att);
+    // publish the partial and count it in; the last arrival merges
+    wait_mem();
+    __syncthreads();
+    if (t == 0) {
+      uint32_t* cp = c.acnt + ((size_t)li * p.max_batch + b) * NKV + h;
+      const uint32_t prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      L.flag = prev == (uint32_t)(nsb - 1);
+    }
+    __syncthreads();
+    if (L.flag) {
+      attn_merge_head<false, BATT_MAX_SPLIT>(c.s, c.part(li, b, h, 0), nsb,
+                                             c.xb(li, p.lay.att) + (size_t)b * H + h * GQA * HD);
+      arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
+    }
+  }
+}
+
+// O projection (split-K, A = attention output read in MFMA layout) + residual -> h1.
+template <int MT>
+__device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  int R0, R1;
+  share(H, c.G, c.w, R0, R1);
+  const int ntile = (R1 - R0 + 15) / 16;
+  const rsrc_t rw = make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES);
+  u32x4 wv[KS];
+  load_w<KS>(rw, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
+  trace_mark(c.s, 2 * xk(li, 3) - 1);
+  // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % 8: B arrivals each
+  wait_handover(c.s, c.ho(li, HO_ATT), c.B, 0);
+  trace_mark(c.s, 2 * xk(li, 3));
+  u32x4 a[MT * KS];
+  load_a<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)c.B * H * 2), c.B, H, wave * KQ, a);
+  uint16_t* h1 = c.xb(li, p.lay.h1);
+  for (int tt = 0; tt < ntile; ++tt) {
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mma_reg<MT, KS>(a, wv, acc);
+    if (tt + 1 < ntile) load_w<KS>(rw, R0 + 16 * (tt + 1), R1, H * 2, wave * KQ, wv);
+    const f32x4 d = reduce_waves<MT>(acc, L);
+    if (wave < MT) {
+      const int row = R0 + tt * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = wave * 16 + (lane >> 4) * 4 + i;
+        if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i])));
+      }
+    }
+    __syncthreads();
+  }
+  arrive(c.ho(li, HO_H1), c.w % N_SUB);
+}
+
+// RMSNorm(h1) -> gate/up GEMM (whole tiles per wave) -> silu(gate) * up -> act.
+template <int MT>
+__device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  int U0, U1, R0, R1;
+  share(INTER, c.G, c.w, U0, U1);
+  share(H, c.G, c.w, R0, R1);
+  const int row0 = 2 * U0, row_end = 2 * U1, ntile = (row_end - row0 + 15) / 16;
+  constexpr int UPT = H / (KS * 32);   // 4 units per tile
+  const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
+  const int nunits = my_tiles * UPT;
+  const rsrc_t rw = make_rsrc(p.w_gu + (size_t)l * 2 * INTER * H, GU_LAYER_BYTES);
+  auto issue = [&](int u, u32x4(&wv)[KS]) {
+    load_w<KS>(rw, u < nunits ? row0 + 16 * (wave + NWAVE * (u / UPT)) : row_end, row_end, H * 2,
+               (u % UPT) * KS * 32, wv);
+  };
+  u32x4 wa[KS], wb[KS];
+  issue(0, wa);
+  issue(1, wb);
+  trace_mark(c.s, 2 * xk(li, 4) - 1);
+  wait_grid(c, li, HO_H1);
+  stage_norm<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+  trace_mark(c.s, 2 * xk(li, 4));
+  uint16_t* act = c.xb(li, p.lay.act);
+  f32x4 acc[MT];
+  auto unit = [&](int u, u32x4(&wv)[KS]) {
+    if (u % UPT == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    mma_lds<MT>(L, (u % UPT) * KS * 32, wv, acc);
+    issue(u + 2, wv);
+    if (u % UPT == UPT - 1) {
+      const int row = row0 + 16 * (wave + NWAVE * (u / UPT)) + (lane & 15);
+      const bool gate = (row & 1) == 0;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float mine = acc[mt][i];
+          const float other = dpp<DPP_XOR1>(mine);   // up (row + 1) for a gate lane
+          const int m = mt * 16 + (lane >> 4) * 4 + i;
+          if (gate && row < row_end && m < c.B)
+            st_dev(act + (size_t)m * INTER + (row >> 1), f2bf(mine / (1.0f + __expf(-mine)) * other));
+        }
+    }
+  };
+  for (int u = 0; u < nunits; u += 2) {
+    unit(u, wa);
+    if (u + 1 < nunits) unit(u + 1, wb);
+  }
+  arrive(c.ho(li, HO_ACT), c.w % N_SUB);
+}
+
+// Down projection (split-K over the waves, A = act read in MFMA layout) + residual -> h2.
+template <int MT>
+__device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  const bool last = li == p.n_layers - 1;
+  int R0, R1;
+  share(H, c.G, c.w, R0, R1);
+  const int ntile = (R1 - R0 + 15) / 16;
+  constexpr int KW = INTER / NWAVE;       // 2048 columns per wave
+  constexpr int UPT = KW / (DKS * 32);    // 8 units per tile
+  const int nunits = ntile * UPT;
+  const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
+  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)c.B * INTER * 2);
+  struct Unit {
+    u32x4 w[DKS];
+    u32x4 a[MT * DKS];
+  };
+  auto issue_w = [&](int u, Unit& un) {
+    load_w<DKS>(rw, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, wave * KW + (u % UPT) * DKS * 32, un.w);
+  };
+  auto issue_a = [&](int u, Unit& un) {
+    load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, wave * KW + (u % UPT) * DKS * 32, un.a);
+  };
+  Unit ua, ub;
+  issue_w(0, ua);
+  issue_w(1, ub);
+  trace_mark(c.s, 2 * xk(li, 5) - 1);
+  wait_grid(c, li, HO_ACT);
+  trace_mark(c.s, 2 * xk(li, 5));
+  issue_a(0, ua);
+  issue_a(1, ub);
+  uint16_t* h2 = c.xb(li, p.lay.h2);
+  f32x4 acc[MT];
+  auto unit = [&](int u, Unit& un) {
+    if (u % UPT == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    mma_reg<MT, DKS>(un.a, un.w, acc);
+    issue_w(u + 2, un);
+    issue_a(u + 2, un);
+    if (u % UPT == UPT - 1) {
+      const f32x4 d = reduce_waves<MT>(acc, L);
+      if (wave < MT) {
+        const int row = R0 + (u / UPT) * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = wave * 16 + (lane >> 4) * 4 + i;
+          if (row < R1 && m < c.B) {
+            const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i]));
+            st_dev(h2 + (size_t)m * H + row, hv);
+            if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  };
+  for (int u = 0; u < nunits; u += 2) {
+    unit(u, ua);
+    if (u + 1 < nunits) unit(u + 1, ub);
+  }
+  arrive(c.ho(li, HO_H2), c.w % N_SUB);
+}
+
+// Order-preserving 64-bit argmax key: larger value first, then lower index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+
+// Final RMSNorm + tied lm_head GEMM (whole tiles per wave) + per-sequence argmax.
+template <int MT>
+__device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int wave = wave_id(), lane = lane_id();
+  int V0, V1, R0, R1;
+  share(VOCAB, c.G, c.w, V0, V1);
+  share(H, c.G, c.w, R0, R1);
+  const int ntile = (V1 - V0 + 15) / 16;
+  constexpr int UPT = H / (KS * 32);
+  const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
+  const int nunits = my_tiles * UPT;
+  const rsrc_t rw = make_rsrc(p.embed, EMBED_BYTES);
+  auto issue = [&](int u, u32x4(&wv)[KS]) {
+    load_w<KS>(rw, u < nunits ? V0 + 16 * (wave + NWAVE * (u / UPT)) : V1, V1, H * 2, (u % UPT) * KS * 32, wv);
+  };
+  u32x4 wa[KS], wb[KS];
+  issue(0, wa);
+  issue(1, wb);
+  trace_mark(c.s, 2 * xk(p.n_layers, 1) - 1);
+  wait_grid(c, p.n_layers - 1, HO_H2);
+  stage_norm<MT>(c, make_rsrc(c.xb(p.n_layers - 1, p.lay.h2), (size_t)c.B * H * 2), false, p.g_final, R0, R1, L);
+  trace_mark(c.s, 2 * xk(p.n_layers, 1));
+  f32x4 acc[MT];
+  float best[MT][4];
+  int bidx[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      best[mt][i] = -INFINITY;
+      bidx[mt][i] = 0x7fffffff;
+    }
+  auto unit = [&](int u, u32x4(&wv)[KS]) {
+    if (u % UPT == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    mma_lds<MT>(L, (u % UPT) * KS * 32, wv, acc);
+    issue(u + 2, wv);
+    if (u % UPT == UPT - 1) {
+      const int row = V0 + 16 * (wave + NWAVE * (u / UPT)) + (lane & 15);
+      if (row < V1) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = mt * 16 + (lane >> 4) * 4 + i;
+            const float v = acc[mt][i];
+            if (m < c.B) {
+              if (p.logits) p.logits[(size_t)m * VOCAB + row] = v;
+              if (v > best[mt][i]) {   // a lane's rows ascend: keeps the lowest index among equal maxima
+                best[mt][i] = v;
+                bidx[mt][i] = row;
+              }
+            }
+          }
+      }
+    }
+  };
+  for (int u = 0; u < nunits; u += 2) {
+    unit(u, wa);
+    if (u + 1 < nunits) unit(u + 1, wb);
+  }
+  // best per token over the 16 lanes of each lane row, then over the waves
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      unsigned long long k = bidx[mt][i] == 0x7fffffff ? 0ull : argmax_key(best[mt][i], bidx[mt][i]);
+#pragma unroll
+      for (int sh = 8; sh >= 1; sh >>= 1) {
+        const unsigned long long o = __shfl_xor(k, sh, 64);
+        k = o > k ? o : k;
+      }
+      if ((lane & 15) == 0) L.key[wave][mt * 16 + (lane >> 4) * 4 + i] = k;
+    }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < c.B) {
+    unsigned long long k = L.key[0][t];
+#pragma unroll
+    for (int w = 1; w < NWAVE; ++w) k = L.key[w][t] > k ? L.key[w][t] : k;
+    if (k != 0ull)
+      __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(p.ws + BWS_KEY0 + (size_t)t * BWS_KEY_STRIDE), k,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int MT>
+__global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
+  __shared__ BLds<MT> L;
+  BCtx c;
+  c.p = &p;
+  uint32_t* ctrl = reinterpret_cast<uint32_t*>(p.ws);
+  c.s.err = ctrl + C_ERR;
+  c.s.timeout = p.timeout_ticks;
+  c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
+  trace_mark(c.s, 0);
+  c.G = gridDim.x;
+  c.w = blockIdx.x;
+  c.B = p.batch;
+  const int t = threadIdx.x;
+  const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const size_t cset = bws_cnt_set(p.max_batch);
+  uint8_t* cnt0 = p.ws + bws_cnt0(p.max_batch);
+  c.hcnt = cnt0 + (size_t)(epoch & 1u) * cset;
+  c.acnt = reinterpret_cast<uint32_t*>(c.hcnt + HCNT_BYTES);
+  {
+    // zero the other counter set for the next launch
+    uint32_t* oc = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
+    int lo, hi;
+    share((int)(cset / 4), c.G, c.w, lo, hi);
+    for (int i = lo + t; i < hi; i += NT) __hip_atomic_store(oc + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (t < c.B) {
+    L.pos[t] = p.pos[t];
+    const int tok = p.tokens ? p.tokens[t] : 0;
+    L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
+  }
+  __syncthreads();
+  bool pos_ok = true;
+  for (int b = 0; b < c.B; ++b) {
+    const int ps = L.pos[b];
+    pos_ok = pos_ok && ps >= 0 && ps < p.s_max && ps < p.rope_rows;
+  }
+  if (!pos_ok && blockIdx.x == 0 && t == 0)
+    __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (pos_ok && t == 0) {
+    // attention items: about two per workgroup over all sequences' KV rows
+    long long total = 0;
+    for (int b = 0; b < c.B; ++b) total += (long long)NKV * (L.pos[b] + 1);
+    long long tr = (total + 2LL * c.G - 1) / (2LL * c.G);
+    tr = (tr + 31) / 32 * 32;
+    if (tr < ATT_MIN_ROWS) tr = ATT_MIN_ROWS;
+    L.cum[0] = 0;
+    for (int b = 0; b < c.B; ++b) {
+      const int n = L.pos[b] + 1;
+      int ns = (int)((n + tr - 1) / tr);
+      ns = ns < BATT_MAX_SPLIT ? ns : BATT_MAX_SPLIT;
+      const int rows = ((n + ns - 1) / ns + 31) / 32 * 32;
+      ns = (n + rows - 1) / rows;
+      L.ns[b] = ns;
+      L.rows[b] = rows;
+      L.cum[b + 1] = L.cum[b] + NKV * ns;
+    }
+  }
+  __syncthreads();
+
+  if (pos_ok) {
+    for (int li = 0; li < p.n_layers; ++li) {
+      phase_qkv<MT>(c, li, L);
+      phase_attn<MT>(c, li, L);
+      phase_o<MT>(c, li, L);
+      phase_gu<MT>(c, li, L);
+      phase_down<MT>(c, li, L);
+    }
+    if (p.do_lm) phase_lm<MT>(c, L);
+  }
+
+  // ---- exit: the last workgroup out publishes the tokens and advances the epoch ----
+  trace_mark(c.s, MK_TRACE_SLOTS - 1);
+  wait_mem();
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(ctrl + C_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    L.flag = prev == (uint32_t)(c.G - 1);
+  }
+  __syncthreads();
+  if (!L.flag || t != 0) return;
+  ctrl[C_EXIT] = 0u;
+  ctrl[C_EPOCH] = epoch + 1u;
+  if (pos_ok) {
+    for (int b = 0; b < c.B; ++b) {
+      if (p.do_lm) {
+        unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + BWS_KEY0 + (size_t)b * BWS_KEY_STRIDE);
+        const unsigned long long key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *kp = 0ull;
+        if (p.next_token) p.next_token[b] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+      }
+      if (p.flags & MK_FLAG_ADVANCE) p.pos[b] = L.pos[b] + 1;
+    }
+  }
+}
+
+struct BDev {
+  int ready;
+  int status;
+  char msg[256];
+};
+BDev g_bdev[64];
+std::mutex g_bdev_mu;
+
+}  // namespace
+
+namespace mk {
+
+int batch_device_check(int dev, char* msg, size_t msg_len) {
+  if (dev < 0 || dev >= 64) {
+    snprintf(msg, msg_len, "device index %d out of range", dev);
+    return MK_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lk(g_bdev_mu);
+  BDev& d = g_bdev[dev];
+  if (!d.ready) {
+    int cus = 0, nb1 = 0, nb2 = 0;
+    d.status = MK_OK;
+    d.msg[0] = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb1, reinterpret_cast<const void*>(mk_batch_kernel<1>), NT, 0) !=
+            hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb2, reinterpret_cast<const void*>(mk_batch_kernel<2>), NT, 0) !=
+            hipSuccess) {
+      d.status = MK_ERR_HIP;
+      snprintf(d.msg, sizeof(d.msg), "device query for the batched kernel failed on device %d", dev);
+    } else if (nb1 < 1 || nb2 < 1) {
+      d.status = MK_ERR_DEVICE;
+      snprintf(d.msg, sizeof(d.msg), "batched kernel cannot be resident on a CU (occupancy %d / %d)", nb1, nb2);
+    } else if (cus < B_MIN_GRID) {
+      d.status = MK_ERR_DEVICE;
+      snprintf(d.msg, sizeof(d.msg), "batched kernel needs >= %d CUs, device %d has %d", B_MIN_GRID, dev, cus);
+    }
+    d.ready = 1;
+  }
+  if (d.status != MK_OK) snprintf(msg, msg_len, "%s", d.msg);
+  return d.status;
+}
+
+hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, int max_batch, int grid,
+                        unsigned long long timeout_ticks) {
+  BParams kp;
+  memset(&kp, 0, sizeof(kp));
+  kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
+  kp.w_o = static_cast<const uint16_t*>(w->w_o);
+  kp.w_gu = static_cast<const uint16_t*>(w->w_gu);
+  kp.w_d = static_cast<const uint16_t*>(w->w_down);
+  kp.embed = static_cast<const uint16_t*>(w->embed);
+  kp.g_final = static_cast<const uint16_t*>(w->norm_final);
+  kp.rope = static_cast<const uint16_t*>(w->rope);
+  for (int i = 0; i < a->n_layers; ++i) {
+    kp.kc[i] = static_cast<uint16_t*>(a->k_cache[i]);
+    kp.vc[i] = static_cast<uint16_t*>(a->v_cache[i]);
+  }
+  kp.tokens = a->tokens;
+  kp.hidden_in = static_cast<const uint16_t*>(a->hidden_in);
+  kp.pos = a->pos;
+  kp.hidden_out = static_cast<uint16_t*>(a->hidden_out);
+  kp.logits = a->logits;
+  kp.next_token = a->next_token;
+  kp.ws = static_cast<uint8_t*>(a->workspace);
+  kp.xch = xch;
+  kp.lay.init(max_batch);
+  kp.batch = a->batch;
+  kp.max_batch = max_batch;
+  kp.first_layer = a->first_layer;
+  kp.n_layers = a->n_layers;
+  kp.s_max = a->s_max;
+  kp.rope_rows = w->rope_rows;
+  kp.do_lm = (a->logits != nullptr || a->next_token != nullptr) ? 1 : 0;
+  kp.flags = a->flags;
+  kp.timeout_ticks = timeout_ticks;
+  kp.trace = static_cast<unsigned long long*>(a->trace);
+  void* args[] = {&kp};
+  const void* fn = a->batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1>)
+                                  : reinterpret_cast<const void*>(mk_batch_kernel<2>);
+  const hipStream_t st = static_cast<hipStream_t>(a->stream);
+  return (a->flags & MK_FLAG_COOPERATIVE) ? hipLaunchCooperativeKernel(fn, dim3(grid), dim3(NT), args, 0, st)
+                                          : hipLaunchKernel(fn, dim3(grid), dim3(NT), args, 0, st);
+}
+
+}  // namespace mk

@@ -454,38 +454,43 @@ __device__ __forceinline__ void attn_split(int n_rows, int max_split, int min_ro
   nsplit = (n_rows + rows - 1) / rows;
 }
 
-// Merge the nsplit partials of one kv head (polled; split s at
-// part_head + s * PART_FLOATS) into the bf16 attention output of its 4 q heads:
+// Merge the nsplit partials of one kv head (split s at part_head + s * PART_FLOATS)
+// into the bf16 attention output of its 4 q heads:
 //   att = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s   (then cast to bf16)
 // Thread t produces q head (t >> 6) of the group, dim t & 63, at att[(t >> 6) * 64 + (t & 63)].
-constexpr int ATT_MERGE_MAX = 8;   // splits a merge reads at most
+// POLL: the partials are polled until none holds the fp32 sentinel; otherwise
+// the caller knows they are complete and they are read once (device scope).
+// MAXS: the most splits a call may pass.
+constexpr int ATT_MERGE_MAX = 8;   // splits the polled merge reads at most
+template <bool POLL = true, int MAXS = ATT_MERGE_MAX>
 __device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* part_head, int nsplit, uint16_t* att) {
   const int t = threadIdx.x, g = t >> 6, d = t & 63;
   const rsrc_t r = make_rsrc(part_head, (size_t)nsplit * PART_FLOATS * 4);
-  uint32_t m[ATT_MERGE_MAX], l[ATT_MERGE_MAX], o[ATT_MERGE_MAX];
+  uint32_t m[MAXS], l[MAXS], o[MAXS];
   const unsigned long long t0 = wall_clock64();
   for (int it = 1;; ++it) {
     bool ok = true;
 #pragma unroll
-    for (int s = 0; s < ATT_MERGE_MAX; ++s) {   // splits >= nsplit read zero (out of range)
+    for (int s = 0; s < MAXS; ++s) {   // splits >= nsplit read zero (out of range)
       const uint32_t base = (uint32_t)(s * PART_FLOATS) * 4u;
       m[s] = ld_dev4(r, base + (uint32_t)g * 4u);
       l[s] = ld_dev4(r, base + (uint32_t)(GQA + g) * 4u);
       o[s] = ld_dev4(r, base + (uint32_t)(2 * GQA + g * HD + d) * 4u);
     }
+    if (!POLL) break;
 #pragma unroll
-    for (int s = 0; s < ATT_MERGE_MAX; ++s) ok = ok && m[s] != 0xffffffffu && l[s] != 0xffffffffu && o[s] != 0xffffffffu;
+    for (int s = 0; s < MAXS; ++s) ok = ok && m[s] != 0xffffffffu && l[s] != 0xffffffffu && o[s] != 0xffffffffu;
     if (__all(ok)) break;
     if (wait_expired(sy, t0, it)) break;
     __builtin_amdgcn_s_sleep(1);
   }
   float M = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < ATT_MERGE_MAX; ++s)
+  for (int s = 0; s < MAXS; ++s)
     if (s < nsplit) M = fmaxf(M, __uint_as_float(m[s]));
   float O = 0.f, Lsum = 0.f;
 #pragma unroll
-  for (int s = 0; s < ATT_MERGE_MAX; ++s) {
+  for (int s = 0; s < MAXS; ++s) {
     const float wgt = s < nsplit ? __expf(__uint_as_float(m[s]) - M) : 0.f;
     Lsum = fmaf(wgt, __uint_as_float(l[s]), Lsum);
     O = fmaf(wgt, __uint_as_float(o[s]), O);

@@ -53,6 +53,7 @@
 #include <mutex>
 
 #include "mk.h"
+#include "mk_batch.h"
 #include "mk_common.h"
 
 namespace {
@@ -83,7 +84,6 @@ constexpr size_t SET_BYTES = (size_t)MK_MAX_LAYERS * X_LAYER;
 constexpr size_t WS_BYTES = CTRL_BYTES;   // the exchange sets live in a separate uncached area
 static_assert(X_ATT % 256 == 0 && X_PART % 256 == 0 && X_LAYER % 256 == 0, "exchange regions must be aligned");
 
-inline size_t ws_bytes_for(int) { return WS_BYTES; }
 
 // ---------------------------------------------------------------------------
 // Kernel parameters
@@ -563,43 +563,78 @@ int device_info(int dev, DeviceInfo* out) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Exchange areas. The per-layer hand-over buffers live in uncached device
-// memory: with it an all-to-all hand-over under a full HBM weight stream took
-// 3.8 us against 6 us in ordinary (L2-cached) memory. Each workspace gets one
-// area of XCH_BYTES, created by its first mk_workspace_init on a device and
-// kept until the process ends: uncached memory that a kernel has read must
-// not be freed while the process runs.
+// Exchange areas, one per initialised workspace and device, created by its
+// first mk_workspace_init there and kept until the process ends.
+//   * batch-1 workspaces: XCH_BYTES of uncached device memory. The per-layer
+//     hand-over buffers are polled there: an all-to-all hand-over under a full
+//     HBM weight stream took 3.8 us against 6 us in ordinary (L2-cached)
+//     memory. Uncached memory that a kernel has read must not be freed while
+//     the process runs.
+//   * batched workspaces (max batch M >= 2): BatchLayout(M).total bytes of
+//     ordinary device memory, whose activation matrices every workgroup reads
+//     through its XCD's L2.
+// A workspace re-initialised with another layout (a new allocation at the
+// same address) gets a matching area; areas it no longer uses stay in the
+// list and are handed to the next workspace that fits.
 constexpr size_t XCH_BYTES = 2 * SET_BYTES;
 struct XchEntry {
-  const void* ws;
+  const void* ws;   // owner (nullptr: spare)
   int dev;
+  int max_batch;    // 1: batch-1 layout
+  size_t bytes;
   uint8_t* xch;
 };
 XchEntry g_xch[256];
 int g_n_xch = 0;
 std::mutex g_xch_mu;
 
-uint8_t* exchange_of(const void* ws, int dev) {
-  std::lock_guard<std::mutex> lk(g_xch_mu);
-  for (int i = 0; i < g_n_xch; ++i)
-    if (g_xch[i].ws == ws && g_xch[i].dev == dev) return g_xch[i].xch;
-  return nullptr;
-}
-
-int exchange_create(const void* ws, int dev, uint8_t** out) {
+bool exchange_of(const void* ws, int dev, XchEntry* out) {
   std::lock_guard<std::mutex> lk(g_xch_mu);
   for (int i = 0; i < g_n_xch; ++i)
     if (g_xch[i].ws == ws && g_xch[i].dev == dev) {
-      *out = g_xch[i].xch;
+      *out = g_xch[i];
+      return true;
+    }
+  return false;
+}
+
+int exchange_create(const void* ws, int dev, int max_batch, XchEntry* out) {
+  const bool uncached = max_batch == 1;
+  size_t need = XCH_BYTES;
+  if (!uncached) {
+    BatchLayout lay;
+    lay.init(max_batch);
+    need = lay.total;
+  }
+  std::lock_guard<std::mutex> lk(g_xch_mu);
+  int mine = -1;
+  for (int i = 0; i < g_n_xch; ++i)
+    if (g_xch[i].ws == ws && g_xch[i].dev == dev) mine = i;
+  if (mine >= 0) {
+    XchEntry& e = g_xch[mine];
+    if ((e.max_batch == 1) == uncached && e.bytes >= need) {
+      e.max_batch = max_batch;
+      *out = e;
       return MK_OK;
     }
+    e.ws = nullptr;   // spare
+  }
+  for (int i = 0; i < g_n_xch; ++i) {
+    XchEntry& e = g_xch[i];
+    if (e.ws == nullptr && e.dev == dev && (e.max_batch == 1) == uncached && e.bytes >= need) {
+      e.ws = ws;
+      e.max_batch = max_batch;
+      *out = e;
+      return MK_OK;
+    }
+  }
   if (g_n_xch == (int)(sizeof(g_xch) / sizeof(g_xch[0])))
     return fail(MK_ERR_WORKSPACE, "too many workspaces initialised in this process (%d)", g_n_xch);
   void* p = nullptr;
-  const hipError_t e = hipExtMallocWithFlags(&p, XCH_BYTES, hipDeviceMallocUncached);
-  if (e != hipSuccess) return fail(MK_ERR_HIP, "exchange area allocation: %s", hipGetErrorString(e));
-  g_xch[g_n_xch++] = XchEntry{ws, dev, static_cast<uint8_t*>(p)};
-  *out = static_cast<uint8_t*>(p);
+  const hipError_t e = uncached ? hipExtMallocWithFlags(&p, need, hipDeviceMallocUncached) : hipMalloc(&p, need);
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "exchange area allocation (%zu bytes): %s", need, hipGetErrorString(e));
+  g_xch[g_n_xch++] = XchEntry{ws, dev, max_batch, need, static_cast<uint8_t*>(p)};
+  *out = g_xch[g_n_xch - 1];
   return MK_OK;
 }
 
@@ -624,8 +659,8 @@ long long mk_wall_clock_hz(int device) {
 }
 
 size_t mk_workspace_bytes(int32_t batch, int32_t s_max) {
-  if (batch != 1 || s_max < 1 || s_max > (1 << 20)) return 0;
-  return ws_bytes_for(s_max);
+  if (batch < 1 || batch > BATCH_MAX || s_max < 1 || s_max > (1 << 20)) return 0;
+  return batch == 1 ? WS_BYTES : batch_ws_bytes(batch);
 }
 
 int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
@@ -636,15 +671,16 @@ int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
     return fail(MK_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, WS_BYTES);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
-  uint8_t* xch = nullptr;
-  int rc = exchange_create(workspace, dev, &xch);
+  XchEntry xe;
+  int rc = exchange_create(workspace, dev, batch_of_ws_bytes(workspace_bytes), &xe);
   if (rc != MK_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t n = workspace_bytes / 16;
   hipLaunchKernelGGL(mk_ws_init_kernel, dim3((int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024)), dim3(256), 0,
                      st, static_cast<u32x4*>(workspace), n, n);
-  hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(xch),
-                     XCH_BYTES / 16, (size_t)0);
+  if (xe.max_batch == 1)   // batch-1 exchange sets start filled with the sentinel
+    hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(xe.xch),
+                       XCH_BYTES / 16, (size_t)0);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MK_ERR_HIP, "workspace init launch: %s", hipGetErrorString(e));
   return MK_OK;
@@ -671,7 +707,7 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
     return fail(MK_ERR_SHAPE, "layers [%d, %d) not within the %d packed layers (max %d)", a->first_layer,
                 a->first_layer + a->n_layers, w->n_layers, MK_MAX_LAYERS);
   if (a->batch < 1) return fail(MK_ERR_SHAPE, "batch %d < 1", a->batch);
-  if (a->batch != 1) return fail(MK_ERR_UNSUPPORTED, "batch %d: this build runs batch 1", a->batch);
+  if (a->batch > BATCH_MAX) return fail(MK_ERR_SHAPE, "batch %d > %d", a->batch, BATCH_MAX);
   if (a->s_max < 1 || a->s_max > w->rope_rows)
     return fail(MK_ERR_SHAPE, "s_max %d must be in [1, rope_rows=%d]", a->s_max, w->rope_rows);
   if (!a->k_cache || !a->v_cache) return fail(MK_ERR_NULL, "k_cache / v_cache array is NULL");
@@ -702,8 +738,24 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   DeviceInfo di;
   const int rc = device_info(dev, &di);
   if (rc != MK_OK) return rc;
-  uint8_t* xch = exchange_of(a->workspace, dev);
-  if (!xch) return fail(MK_ERR_WORKSPACE, "workspace was not initialised with mk_workspace_init on device %d", dev);
+  XchEntry xe;
+  if (!exchange_of(a->workspace, dev, &xe))
+    return fail(MK_ERR_WORKSPACE, "workspace was not initialised with mk_workspace_init on device %d", dev);
+  if (a->batch > xe.max_batch)
+    return fail(MK_ERR_WORKSPACE, "batch %d exceeds the workspace's batch %d (mk_workspace_bytes)", a->batch,
+                xe.max_batch);
+  if (xe.max_batch > 1) {
+    // batched layout: MFMA kernel (mk_batch.hip) for every batch size on this workspace
+    if (a->workspace_bytes < batch_ws_bytes(xe.max_batch))
+      return fail(MK_ERR_WORKSPACE, "workspace %zu bytes < %zu it was initialised with", a->workspace_bytes,
+                  batch_ws_bytes(xe.max_batch));
+    const int brc = batch_device_check(dev, g_msg, sizeof(g_msg));
+    if (brc != MK_OK) return brc;
+    const hipError_t be = batch_launch(w, a, xe.xch, xe.max_batch, di.grid, di.ticks_per_s * 2ull);
+    if (be != hipSuccess) return fail(MK_ERR_HIP, "batched kernel launch failed: %s", hipGetErrorString(be));
+    return MK_OK;
+  }
+  uint8_t* xch = xe.xch;
 
   KParams kp;
   memset(&kp, 0, sizeof(kp));

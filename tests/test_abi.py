@@ -39,6 +39,11 @@ def test_workspace_size(lib):
     assert lib.mk_workspace_bytes(1, 8192) >= lib.mk_workspace_bytes(1, 1024)
     assert lib.mk_workspace_bytes(0, 1024) == 0
     assert lib.mk_workspace_bytes(1, 0) == 0
+    # batched layouts (2..32 sequences): larger batches need more, 33 is unsupported
+    sizes = [lib.mk_workspace_bytes(b, 4096) for b in range(1, 33)]
+    assert all(s > 0 for s in sizes)
+    assert sizes == sorted(sizes) and sizes[1] > sizes[0]
+    assert lib.mk_workspace_bytes(33, 4096) == 0
 
 
 def _args(**over):
@@ -67,7 +72,7 @@ def _weights(**over):
     (dict(n_layers=17), -2),
     (dict(first_layer=15, n_layers=2), -2),
     (dict(batch=0), -2),
-    (dict(batch=4), -4),
+    (dict(batch=33), -2),
     (dict(s_max=0), -2),
     (dict(s_max=9000), -2),
     (dict(tokens=None), -1),
