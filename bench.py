@@ -16,6 +16,14 @@ on the kernel's stream, the HBM roofline of the megakernel (algorithmic bytes
 per step / mean step time vs 8 TB/s), and a CPU baseline: the oracle's fp32
 decode step timed on this host's cores on a bounded sample.
 
+``--config c4`` / ``--config c5`` time the batched step instead (BASELINE
+configs 4 and 5; not the headline line): batch 8 with ragged KV lengths
+(prompt lengths uniform in [512, 3840], seed 0, so that 256 steps fit the
+4096-row caches) and batch 32 at KV lengths 8064..8191 of 8192-row caches.
+Their caches below each sequence's start position hold N(0,1) bf16 values
+instead of prefilled K/V (the step's cost does not depend on the values);
+tok/s counts every sequence's token.
+
 ``--gpus N`` with N > 1 exits: this benchmark runs on one GPU.
 """
 
@@ -39,6 +47,10 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_JSON = REPO / "profiles" / "mk_decode_kernel_c3_bs1_traffic.json"
 PROMPT = 384
 S_MAX = 1024
+BATCH_CONFIGS = {
+    "c4": dict(batch=8, s_max=4096, steps=256, lo=512, hi=3840),
+    "c5": dict(batch=32, s_max=8192, steps=128, lo=8192 - 128, hi=8192 - 128),
+}
 
 
 def log(*a):
@@ -86,6 +98,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=24)
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", choices=["c3", "c4", "c5"], default="c3",
+                    help="c3: the headline bs=1 decode; c4/c5: the batched configurations")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES (HBM counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -101,6 +115,9 @@ def main():
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
+    if args.config != "c3":
+        run_batched(args, BATCH_CONFIGS[args.config])
+        return
     if not 1 <= args.steps <= S_MAX - PROMPT:
         sys.exit(f"--steps must be in [1, {S_MAX - PROMPT}]")
 
@@ -183,6 +200,85 @@ def main():
         from mk_weights import synthetic_state_dict
         sd = synthetic_state_dict(seed=0)
         result["cpu_baseline"] = cpu_baseline(sd, args.cpu_steps, args.cpu_budget_s)
+    print(json.dumps(result), flush=True)
+
+
+def run_batched(args, cfg):
+    """A batched decode configuration (BASELINE configs 4 and 5)."""
+    import torch
+    import mk_lib
+    from mk_config import LLAMA_3_2_1B, step_bytes
+    from mk_weights import pack_for_megakernel, random_token_ids, synthetic_state_dict
+
+    B, S, K = cfg["batch"], cfg["s_max"], min(args.steps, cfg["steps"])
+    g = torch.Generator().manual_seed(0)
+    starts = [int(torch.randint(cfg["lo"], cfg["hi"] + 1, (1,), generator=g)) for _ in range(B)]
+    t0 = time.perf_counter()
+    sd = synthetic_state_dict(seed=0)
+    packed = pack_for_megakernel(sd, LLAMA_3_2_1B, device="cuda", rope_rows=S)
+    del sd
+    w = mk_lib.weights_struct(packed)
+    # caches: N(0,1) bf16 (rows at and above a sequence's start are rewritten by the steps)
+    kv = torch.empty(16, 2, B, 8, S, 64, dtype=torch.bfloat16, device="cuda")
+    gd = torch.Generator(device="cuda").manual_seed(1)
+    for l in range(16):
+        kv[l].normal_(generator=gd)
+    ws = mk_lib.Workspace(B, S, torch.device("cuda"))
+    pos = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    toks = random_token_ids(B, seed=0).to(device="cuda", dtype=torch.int32)
+    logits = torch.empty(B, LLAMA_3_2_1B.vocab, dtype=torch.float32, device="cuda")
+    step = mk_lib.StepLauncher(w, ws, [kv[l, 0] for l in range(16)], [kv[l, 1] for l in range(16)], pos,
+                               tokens=toks, logits=logits, next_token=toks, flags=mk_lib.MK_FLAG_ADVANCE, batch=B)
+    torch.cuda.synchronize()
+    log(f"[bench] {args.config}: batch {B}, cache rows {S}, start positions {min(starts)}..{max(starts)}; "
+        f"ready in {time.perf_counter() - t0:.1f}s")
+    pos0, tok0 = pos.clone(), toks.clone()
+    for _ in range(min(args.warmup, K)):
+        step.launch()
+    torch.cuda.synchronize()
+    pos.copy_(pos0)
+    toks.copy_(tok0)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    evs[0].record()
+    for i in range(K):
+        step.launch()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    bits = ws.read_device_error()
+    if bits:
+        sys.exit(f"device error bits 0x{bits:x}")
+    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
+    mean_ms = sum(step_ms) / K
+    bytes_per_step = sum(step_bytes(16, [p + i for p in starts], lm_head=True) for i in range(K)) / K
+    achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
+    result = {
+        "metric": f"batched decode tok/s (all sequences), Llama-3.2-1B, {args.config.upper()}; HBM GB/s",
+        "value": round(B * K / wall, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "p50_step_ms": round(statistics.median(step_ms), 4),
+        "p90_step_ms": round(sorted(step_ms)[int(0.9 * (K - 1))], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights seed 0, N(0,1) bf16 KV cache below each start "
+                "position, uniform-random token ids)",
+        "config": {"workload": f"{args.config.upper()}: Llama-3.2-1B decode, batch {B}, {S}-row KV caches, "
+                               f"start positions {min(starts)}..{max(starts)}, {K} greedy steps",
+                   "batch": B, "max_context_length": S, "start_positions": starts, "n_layers": 16},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_step": int(bytes_per_step),
+                     "kernel": f"mk_batch_kernel<{1 if B <= 16 else 2}>"},
+        "cpu_baseline": None,
+    }
     print(json.dumps(result), flush=True)
 
 
