@@ -400,6 +400,12 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     const int ps = L.pos[b], rows = L.rows[b];
     const int j0 = sp * rows, j1 = min(j0 + rows, ps + 1);
     const bool fresh = ps >= j0 && ps < j1;
+    // the item's cached rows do not depend on this step: their first group is issued before the wait for q
+    const size_t head = (size_t)(b * NKV + h) * p.s_max * HD;
+    AttnRows ar;
+    ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
+    AttnGroup g0;
+    ar.load(0, g0);
     if (wave_id() == 0) {
       if (!waited) {
         trace_mark(c.s, 2 * xk(li, 2) - 1);
@@ -417,8 +423,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     }
     waited = true;
     __syncthreads();
-    const size_t head = (size_t)(b * NKV + h) * p.s_max * HD;
-    attn_item(p.kc[li] + head, p.vc[li] + head, p.s_max, L.q, j0, min(j1, ps), fresh, c.part(li, b, h, sp), L.att);
+    attn_item(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
     // publish the partial and count it in; the last arrival merges
     wait_mem();
     __syncthreads();

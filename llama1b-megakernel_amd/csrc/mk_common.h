@@ -179,13 +179,19 @@ __device__ __forceinline__ bool wait_expired(const Sync& s, unsigned long long t
 // OOB offsets read zero and count as ready) until the whole wave sees no
 // sentinel. A piece seen complete is not read again (its offset turns OOB),
 // so waiting consumers only re-read what is still missing. Called by full waves.
-template <int N>
-__device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_t (&off)[N], u32x4 (&v)[N]) {
+// idle() runs before each round of polls (a caller issues background loads there).
+struct NoIdle {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <int N, class Idle = NoIdle>
+__device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_t (&off)[N], u32x4 (&v)[N],
+                                          Idle&& idle = Idle()) {
   const unsigned long long t0 = wall_clock64();
   bool done[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) done[i] = false;
   for (int it = 1;; ++it) {
+    idle();
     u32x4 t[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) t[i] = ld_dev16(r, done[i] ? OOB : off[i]);
@@ -207,8 +213,9 @@ __device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_
 // Stage a bf16 vector of PER_WAVE*4 chunks of 512 elements into LDS: wave w
 // copies chunks w, w+4, ... Exchange buffers are polled; final data (the
 // embedding row, hidden_in) is read directly. The caller synchronises.
-template <int PER_WAVE>
-__device__ __forceinline__ void stage_vec(const Sync& s, const uint16_t* src, bool polled, uint16_t* lds) {
+template <int PER_WAVE, class Idle = NoIdle>
+__device__ __forceinline__ void stage_vec(const Sync& s, const uint16_t* src, bool polled, uint16_t* lds,
+                                          Idle&& idle = Idle()) {
   const int lane = lane_id(), wave = wave_id();
   const rsrc_t r = make_rsrc(src, (size_t)PER_WAVE * NWAVE * 1024);
   uint32_t off[PER_WAVE];
@@ -216,7 +223,7 @@ __device__ __forceinline__ void stage_vec(const Sync& s, const uint16_t* src, bo
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) off[i] = (uint32_t)((wave + NWAVE * i) * 1024 + lane * 16);
   if (polled) {
-    poll_bf16<PER_WAVE>(s, r, off, v);
+    poll_bf16<PER_WAVE>(s, r, off, v, idle);
   } else {
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) v[i] = ld16(r, off[i]);
@@ -294,20 +301,51 @@ __device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rro
 }
 
 
+// K/V rows of an attention item streamed ATT_GROUP at a time: thread t loads
+// row (t >> 3) of each 32-row round, dims (t & 7)*8 .. +7, of K and of V.
+// Rows >= jc read zero through OOB offsets and are flagged invalid.
+constexpr int ATT_R = ATT_GROUP / 32;
+struct AttnGroup {
+  u32x4 k[ATT_R], v[ATT_R];
+  bool valid[ATT_R];
+};
+struct AttnRows {
+  rsrc_t rk, rv;
+  int j0, jc;
+  __device__ __forceinline__ void init(const uint16_t* kc_head, const uint16_t* vc_head, int s_max, int j0_,
+                                       int jc_) {
+    const size_t head_bytes = (size_t)s_max * HD * 2;
+    rk = make_rsrc(kc_head, head_bytes);
+    rv = make_rsrc(vc_head, head_bytes);
+    j0 = j0_;
+    jc = jc_;
+  }
+  __device__ __forceinline__ int ngroups() const { return jc > j0 ? (jc - j0 + ATT_GROUP - 1) / ATT_GROUP : 0; }
+  __device__ __forceinline__ void load(int gi, AttnGroup& g) const {
+    const int rl = threadIdx.x >> 3, ch = threadIdx.x & 7;
+#pragma unroll
+    for (int r = 0; r < ATT_R; ++r) {
+      const int j = j0 + gi * ATT_GROUP + 32 * r + rl;
+      g.valid[r] = j < jc;
+      const uint32_t off = g.valid[r] ? (uint32_t)(j * HD + ch * 8) * 2u : OOB;
+      g.k[r] = ld_stream(rk, off);
+      g.v[r] = ld_stream(rv, off);
+    }
+  }
+};
+
 // One attention work item: one kv head of one sequence, cached KV rows
 // [j0, jc) plus, if `fresh`, the new row (from LDS), for the 4 q heads of the
-// group (GQA). kc_head / vc_head: the head's cache rows, bf16 [s_max][64];
-// q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
+// group (GQA). `rows` describes the head's cache rows (bf16 [s_max][64] for K
+// and for V); `first` holds its first group, already issued with rows.load(0)
+// (the cached rows do not depend on the current step, so a caller issues them
+// before it waits for q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
 // Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
 // of it; rows stream in groups of ATT_GROUP with an online softmax. Writes
 // the item's partial (m[4], l[4], o[4][64]) unnormalised, relative to m.
-__device__ __forceinline__ void attn_item(const uint16_t* kc_head, const uint16_t* vc_head, int s_max,
-                                          const uint16_t* q_lds, int j0, int jc, bool fresh, float* part,
-                                          AttnShared& sh) {
+__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first, const uint16_t* q_lds, bool fresh,
+                                          float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
-  const size_t head_bytes = (size_t)s_max * HD * 2;
-  const rsrc_t rk = make_rsrc(kc_head, head_bytes);
-  const rsrc_t rv = make_rsrc(vc_head, head_bytes);
   u32x4 q[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(q_lds + g * HD + ch * 8);
@@ -319,7 +357,7 @@ __device__ __forceinline__ void attn_item(const uint16_t* kc_head, const uint16_
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  constexpr int R = ATT_GROUP / 32;
+  constexpr int R = ATT_R;
   auto consume = [&](const u32x4(&kk)[R], const u32x4(&vv)[R], const bool(&valid)[R]) {
     float sc[R][GQA];
 #pragma unroll
@@ -356,34 +394,14 @@ __device__ __forceinline__ void attn_item(const uint16_t* kc_head, const uint16_
     }
   };
   // cached rows in groups of ATT_GROUP, the next group's loads in flight while one is consumed
-  auto load_group = [&](int base, u32x4(&kk)[R], u32x4(&vv)[R], bool(&valid)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int j = base + 32 * r + rl;
-      valid[r] = j < jc;
-      const uint32_t off = valid[r] ? (uint32_t)(j * HD + ch * 8) * 2u : OOB;
-      kk[r] = ld_stream(rk, off);
-      vv[r] = ld_stream(rv, off);
-    }
-  };
-  const int ngroups = jc > j0 ? (jc - j0 + ATT_GROUP - 1) / ATT_GROUP : 0;
-  u32x4 kA[R], vA[R];
-  bool validA[R];
-  if (ngroups > 0) load_group(j0, kA, vA, validA);
+  const int ngroups = rows.ngroups();
+  AttnGroup& A = first;
   for (int gi = 0; gi < ngroups; ++gi) {
-    u32x4 kB[R], vB[R];
-    bool validB[R];
+    AttnGroup B;
     const bool more = gi + 1 < ngroups;
-    if (more) load_group(j0 + (gi + 1) * ATT_GROUP, kB, vB, validB);
-    consume(kA, vA, validA);
-    if (more) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        kA[r] = kB[r];
-        vA[r] = vB[r];
-        validA[r] = validB[r];
-      }
-    }
+    if (more) rows.load(gi + 1, B);
+    consume(A.k, A.v, A.valid);
+    if (more) A = B;
   }
   if (fresh) {   // the new row: row-lane 0 of the first round
     u32x4 kk[R], vv[R];

@@ -38,6 +38,12 @@
 //   * before polling for its input each wave has already issued the first
 //     ring of the phase's weight loads (they do not depend on the
 //     activations), so the hand-over latency overlaps HBM traffic;
+//   * the attention and O hand-overs leave HBM mostly idle, so during them
+//     each wave copies the first 4 gate/up pairs of its GU share (32 KiB)
+//     straight from HBM into LDS (buffer loads with the LDS bit), two 1 KiB
+//     chunks per poll round so the polls, which complete behind earlier
+//     loads, are not held up; attention items issue their cached K/V rows
+//     before they wait for q;
 //   * GEMVs are bf16 x bf16 -> fp32 with v_dot2_f32_bf16, reduced across the
 //     wave with DPP row operations and four lane reads (bs=1 is
 //     bandwidth-bound: no MFMA);
@@ -61,7 +67,8 @@ namespace {
 using namespace mk;
 
 constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
-static_assert(ATT_MAX_SPLIT <= ATT_MERGE_MAX, "a merge reads at most ATT_MERGE_MAX splits");
+constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
+constexpr int GU_LDS_STEP = 2;             // 1 KiB chunks of that copy issued per hand-over poll
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -177,6 +184,47 @@ __device__ __forceinline__ Span wave_span(int lo, int hi) {
   return Span{lo + a, b - a};
 }
 
+// A wave's background copy of `total` contiguous 1 KiB chunks of weights
+// (starting at byte off0 of resource rs) straight from HBM into its own LDS
+// region, issued a few chunks at a time; chunk k lands at dst + k*1024.
+// The wave waits for them with s_waitcnt vmcnt before reading the region.
+struct LdsPrefetch {
+  rsrc_t rs;
+  uint32_t off0, stride;   // row r of the copy starts at off0 + r*stride
+  int kch;                 // 1 KiB chunks per row
+  int total, next;
+  uint8_t* dst;
+  __device__ __forceinline__ void init(rsrc_t r, uint32_t o0, uint32_t st, int chunks_per_row, int rows,
+                                       uint8_t* lds) {
+    rs = r;
+    off0 = o0;
+    stride = st;
+    kch = chunks_per_row;
+    total = rows * chunks_per_row;
+    next = 0;
+    dst = lds;
+  }
+  __device__ __forceinline__ void issue(int n) {
+    const int end = min(total, next + n);
+    for (; next < end; ++next)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(dst + next * 1024), 16,
+          off0 + (uint32_t)(next / kch) * stride + (uint32_t)(next % kch) * 1024u + (uint32_t)lane_id() * 16u, 0, 0,
+          AUX_NT);
+  }
+};
+
+// GU pairs [0, GU_LDS_PAIRS) of this wave's share, HBM -> L.gu[wave] (pair j at j*8 KiB).
+struct GuPrefetch : LdsPrefetch {
+  __device__ __forceinline__ void start(const uint16_t* w_gu_layer, int G, int w, uint8_t* region) {
+    int U0, U1;
+    share(INTER, G, w, U0, U1);
+    const Span gp = wave_span(U0, U1);
+    init(make_rsrc(w_gu_layer, GU_LAYER_BYTES), (uint32_t)gp.lo * (2 * H * 2), 2 * H * 2, 8,
+         min(gp.n, GU_LDS_PAIRS), region);
+  }
+};
+
 // ---------------------------------------------------------------------------
 // The megakernel
 // ---------------------------------------------------------------------------
@@ -190,6 +238,7 @@ struct Lds {
   float best[NWAVE];
   int bidx[NWAVE];
   int last;
+  __attribute__((aligned(16))) uint8_t gu[NWAVE][GU_LDS_PAIRS * 8192];   // GU pairs copied ahead (per wave)
 };
 
 struct Ctx {
@@ -212,31 +261,44 @@ struct Ctx {
 // Trace exchange index of phase `ph` (1 QKV, 2 ATTN, 3 O, 4 GU, 5 DOWN) of run-layer li.
 __device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
 
-// QKV phase of run-layer li (stack layer l): RMSNorm, GEMV, RoPE; q and the
-// fresh K/V row to the exchange buffer, the K/V row also into the caches.
-__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L) {
+// The wave's QKV weight rows of run-layer li: rows 2*P0 + wave + 4*j, j < n.
+__device__ __forceinline__ void qkv_rows(const Ctx& c, int li, rsrc_t& r, uint32_t& off0, int& n) {
   const KParams& p = *c.p;
-  const int l = p.first_layer + li;
+  int P0, P1;
+  share(QKV_PAIRS, c.G, c.w, P0, P1);
+  r = make_rsrc(p.w_qkv + (size_t)(p.first_layer + li) * QKV_ROWS * H, QKV_LAYER_BYTES);
+  off0 = (uint32_t)(2 * P0 + wave_id()) * (H * 2);
+  n = wave_count(0, 2 * (P1 - P0));
+}
+
+// QKV phase of run-layer li: RMSNorm, GEMV, RoPE; q and the fresh K/V row to
+// the exchange buffer, the K/V row also into the caches. idle() runs between
+// the polls for the layer input.
+template <class Idle>
+__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
+  const KParams& p = *c.p;
   const int wave = wave_id();
   int P0, P1;
   share(QKV_PAIRS, c.G, c.w, P0, P1);
-  const int nrows = 2 * (P1 - P0);
+  rsrc_t wr;
+  uint32_t woff;
+  int wn;
+  qkv_rows(c, li, wr, woff, wn);
   RowStream<4, 4> rs;
-  rs.start(make_rsrc(p.w_qkv + (size_t)l * QKV_ROWS * H, QKV_LAYER_BYTES),
-           (uint32_t)(2 * P0 + wave) * (H * 2), NWAVE * H * 2, wave_count(0, nrows));
+  rs.start(wr, woff, NWAVE * H * 2, wn);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li == 0) stage_vec<1>(c.s, c.x_in, false, L.x);
-  else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x);
+  else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x, idle);
   __syncthreads();
   trace_mark(c.s, 2 * xk(li, 1));
   u32x4 xs[4];
   lds_x2048(L.x, xs);
   rmsnorm2048(xs, nullptr);
-  rs.run([&](const u32x4(&wv)[4]) { return dot2048(wv, xs); },
-         [&](int r, float part) {
-           const float v = wave_sum(part);
-           if (lane_id() == 0) L.val[wave + NWAVE * r] = v;
-         });
+  auto emit = [&](int r, float part) {
+    const float v = wave_sum(part);
+    if (lane_id() == 0) L.val[wave + NWAVE * r] = v;
+  };
+  rs.run([&](const u32x4(&wv)[4]) { return dot2048(wv, xs); }, emit);
   __syncthreads();
   const uint16_t* rrow = p.rope + (size_t)c.pos * (2 * HD);
   uint16_t* xq = c.xb(li, X_QKV);
@@ -273,6 +335,12 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     const int h = it / nsplit, sp = it % nsplit;
     const int j0 = sp * rows, j1 = min(j0 + rows, c.n_rows);
     const bool fresh = c.pos >= j0 && c.pos < j1;
+    // the item's cached rows do not depend on this step: their first group is issued before the wait for q
+    AttnRows ar;
+    ar.init(c.p->kc[li] + (size_t)h * c.p->s_max * HD, c.p->vc[li] + (size_t)h * c.p->s_max * HD, c.p->s_max, j0,
+            min(j1, c.pos));
+    AttnGroup g0;
+    ar.load(0, g0);
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2) - 1);
     if (wave_id() == 0) {
       // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
@@ -288,10 +356,10 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     }
     __syncthreads();
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2));
-    attn_item(c.p->kc[li] + (size_t)h * c.p->s_max * HD, c.p->vc[li] + (size_t)h * c.p->s_max * HD, c.p->s_max,
-              L.q, j0, min(j1, c.pos), fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
+    attn_item(ar, g0, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
     if (sp == 0)
-      attn_merge_head(c.s, c.part(li) + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS, nsplit, c.xb(li, X_ATT) + h * GQA * HD);
+      attn_merge_head<true, ATT_MAX_SPLIT>(c.s, c.part(li) + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS, nsplit,
+                                           c.xb(li, X_ATT) + h * GQA * HD);
   }
 }
 
@@ -337,7 +405,14 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
       const bool last = li == p.n_layers - 1;
-      phase_qkv(c, li, L);
+      // The first GU_LDS_PAIRS gate/up pairs of each wave's GU share go HBM -> LDS
+      // directly while the layer waits for its input and its attention output,
+      // a few chunks per poll round: the hand-over polls queue behind them
+      // (vector loads complete in order), so the copy is spread out.
+      GuPrefetch gpf;
+      gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, G, w, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
+      auto gidle = [&]() { gpf.issue(GU_LDS_STEP); };
+      phase_qkv(c, li, L, gidle);
       phase_attn(c, li, L);
 
       // ---- O projection + residual -> h1 ----
@@ -346,7 +421,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         const Span sp = wave_span(R0, R1);
         os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
         trace_mark(c.s, 2 * xk(li, 3) - 1);
-        stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v);
+        stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, gidle);
+        gpf.issue(GU_LDS_PAIRS * 8);   // whatever the waits left
         __syncthreads();
         trace_mark(c.s, 2 * xk(li, 3));
         u32x4 xs[4];
@@ -367,8 +443,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         share(INTER, G, w, U0, U1);
         RowStream<4, 8> gs;
         const Span sp = wave_span(U0, U1);
-        gs.start(make_rsrc(p.w_gu + (size_t)l * 2 * INTER * H, GU_LAYER_BYTES), (uint32_t)sp.lo * (2 * H * 2),
-                 2 * H * 2, sp.n);
+        const int n_lds = gpf.total / 8;   // pairs [0, n_lds) are in LDS
+        gs.start(make_rsrc(p.w_gu + (size_t)l * 2 * INTER * H, GU_LAYER_BYTES),
+                 (uint32_t)(sp.lo + n_lds) * (2 * H * 2), 2 * H * 2, sp.n - n_lds);
         trace_mark(c.s, 2 * xk(li, 4) - 1);
         stage_vec<1>(c.s, c.xb(li, X_H1), true, L.h1);
         __syncthreads();
@@ -379,20 +456,31 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         uint16_t* act = c.xb(li, X_ACT);
         struct GU2 { float g, u; };
         float mine = 0.f;   // lane r: silu(gate) * up of the wave's pair r
-        gs.run([&](const u32x4(&wv)[8]) {
-                 float g0 = dot8(wv[0], xs[0], 0.f), g1 = dot8(wv[1], xs[1], 0.f);
-                 float u0 = dot8(wv[4], xs[0], 0.f), u1 = dot8(wv[5], xs[1], 0.f);
-                 g0 = dot8(wv[2], xs[2], g0);
-                 g1 = dot8(wv[3], xs[3], g1);
-                 u0 = dot8(wv[6], xs[2], u0);
-                 u1 = dot8(wv[7], xs[3], u1);
-                 return GU2{g0 + g1, u0 + u1};
-               },
-               [&](int r, GU2 part) {
-                 const float gv = wave_sum(part.g);
-                 const float uv = wave_sum(part.u);
-                 if (lane == r) mine = gv / (1.0f + __expf(-gv)) * uv;
-               });
+        auto gu_dot = [&](const u32x4(&wv)[8]) {
+          float g0 = dot8(wv[0], xs[0], 0.f), g1 = dot8(wv[1], xs[1], 0.f);
+          float u0 = dot8(wv[4], xs[0], 0.f), u1 = dot8(wv[5], xs[1], 0.f);
+          g0 = dot8(wv[2], xs[2], g0);
+          g1 = dot8(wv[3], xs[3], g1);
+          u0 = dot8(wv[6], xs[2], u0);
+          u1 = dot8(wv[7], xs[3], u1);
+          return GU2{g0 + g1, u0 + u1};
+        };
+        auto gu_emit = [&](int r, GU2 part) {
+          const float gv = wave_sum(part.g);
+          const float uv = wave_sum(part.u);
+          if (lane == r) mine = gv / (1.0f + __expf(-gv)) * uv;
+        };
+        wait_mem();   // this wave's LDS copy (and the ring) have landed
+        {
+          const uint8_t* src = L.gu[wave];
+          for (int j = 0; j < n_lds; ++j) {
+            u32x4 wv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
+            gu_emit(j, gu_dot(wv));
+          }
+        }
+        gs.run(gu_dot, [&](int r, GU2 part) { gu_emit(n_lds + r, part); });
         if (lane < sp.n) st_dev(act + sp.lo + lane, f2bf(mine));
       }
 
