@@ -239,9 +239,7 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
       }
     }
   }
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
+  ss = sum_lanes8(ss);
   const float inv = rsqrtf(ss * (1.0f / H) + EPS);
   if (rowv) {
     for (int i = 0; i < 32; ++i) {

@@ -56,8 +56,17 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
-__device__ __forceinline__ float rbf(float f) { return __uint_as_float(f2bf(f) << 16); }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+// Two floats -> packed bf16x2 with the hardware conversion (v_cvt_pk_bf16_f32,
+// round to nearest even, equal to f2bf bit for bit except that a NaN keeps
+// its payload, so it may be 0xffff): for values that stay in registers.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+// fp32 rounded to bf16 precision (hardware conversion; registers only).
+__device__ __forceinline__ float rbf(float f) { return __uint_as_float(cvt_bf2(f, 0.f) << 16); }
 // fp32 for an exchange buffer: NaN canonicalised (never the 0xffffffff sentinel).
 __device__ __forceinline__ float canon(float f) { return f != f ? __uint_as_float(0x7fc00000u) : f; }
 
@@ -88,6 +97,148 @@ constexpr int DPP_XOR1 = 0xb1;      // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4e;      // quad_perm [2,3,0,1]
 constexpr int DPP_ROR4 = 0x124;     // row_ror:4 (rotate within 16 lanes)
 constexpr int DPP_ROR8 = 0x128;     // row_ror:8
+
+constexpr int DPP_HALF_MIRROR = 0x141;  // row_half_mirror: lane i of each 8-lane group reads lane 7-i
+
+// Sum over each aligned group of 8 lanes (8k .. 8k+7), in every lane of the
+// group: after the two quad steps both quads of the group are uniform, so the
+// half-row mirror adds the other quad (the same sums as xor-4 butterflies).
+__device__ __forceinline__ float sum_lanes8(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  return v + dpp<DPP_HALF_MIRROR>(v);
+}
+
+// Lane i's value and lane i^16 / i^32's (gfx950 permlane swaps). The swap
+// exchanges the odd 16-lane rows of its first register with the even rows of
+// its second (or the upper 32 lanes of the first with the lower 32 of the
+// second); with both registers holding v it leaves
+// {v of rows 0,0,2,2 | rows 1,1,3,3} or {v of lanes 0-31 twice | 32-63 twice}.
+// Inline assembly: both registers are read and written, which the compiler's
+// builtin for these instructions does not model here (it aliases the two
+// results). The s_nops cover the VALU-write -> permlane-read hazard.
+struct Pair {
+  float a, b;
+};
+__device__ __forceinline__ Pair xor16_pair(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return Pair{a, b};
+}
+__device__ __forceinline__ Pair xor32_pair(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return Pair{a, b};
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const Pair p = xor16_pair(v);
+  return p.a + p.b;
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const Pair p = xor32_pair(v);
+  return p.a + p.b;
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const Pair p = xor16_pair(v);
+  return fmaxf(p.a, p.b);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const Pair p = xor32_pair(v);
+  return fmaxf(p.a, p.b);
+}
+// Sum / max over the 8 lanes of the wave with the same lane & 7 (lane ^ 8, ^16, ^32).
+__device__ __forceinline__ float sum_stride8(float v) {
+  v += dpp<DPP_ROR8>(v);   // within a 16-lane row, lane i^8
+  return add_xor32(add_xor16(v));
+}
+__device__ __forceinline__ float max_stride8(float v) {
+  v = fmaxf(v, dpp<DPP_ROR8>(v));
+  return max_xor32(max_xor16(v));
+}
+
+// Transposed reduction of N = 1, 2, 4, 8 or 16 per-lane partial sums (one per
+// GEMV row) over the 64 lanes: one exchange step per lane bit halves both the
+// values per lane and the lanes per row, so N rows cost about 2N + 8
+// instructions instead of N full wave sums. Returns, in lane i, the full sum
+// of row reduce_row<N>(i); each row's sum is held by 64/N lanes.
+//   bit 5: permlane32 swap of rows (k, k+N/2)   bit 4: permlane16 swap
+//   bit 3: DPP row_ror:8 (lane ^ 8)             bit 2: DPP row_half_mirror (lane ^ 7)
+// at each step the lanes with the bit clear keep the lower row of the pair.
+// The remaining lane bits are then summed with plain steps (quads first).
+template <int N>
+__device__ __forceinline__ int reduce_row(int lane) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "N rows per reduction");
+  int r = 0, w = N;
+  if (w > 1) { w >>= 1; r += ((lane >> 5) & 1) * w; }
+  if (w > 1) { w >>= 1; r += ((lane >> 4) & 1) * w; }
+  if (w > 1) { w >>= 1; r += ((lane >> 3) & 1) * w; }
+  if (w > 1) { w >>= 1; r += ((lane >> 2) & 1) * w; }
+  return r;
+}
+__device__ __forceinline__ Pair swap32(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return Pair{a, b};
+}
+__device__ __forceinline__ Pair swap16(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return Pair{a, b};
+}
+template <int N>
+__device__ __forceinline__ float reduce_rows(const float (&in)[N]) {
+  const int lane = threadIdx.x & 63;
+  float v[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = in[k];
+  int n = N;
+  // bit 5: lanes 0-31 end up with rows k, lanes 32-63 with rows k + n/2
+  if (n > 1) {
+    n >>= 1;
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+      const Pair p = swap32(v[k], v[k + N / 2]);
+      v[k] = p.a + p.b;
+    }
+  } else {
+    v[0] = add_xor32(v[0]);
+  }
+  // bit 4
+  if (n > 1) {
+    n >>= 1;
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      const Pair p = swap16(v[k], v[k + N / 4]);
+      v[k] = p.a + p.b;
+    }
+  } else {
+    v[0] = add_xor16(v[0]);
+  }
+  // bit 3 (lane ^ 8 within a 16-lane row)
+  const bool b3 = lane & 8, b2 = lane & 4;
+  if (n > 1) {
+    n >>= 1;
+#pragma unroll
+    for (int k = 0; k < N / 8; ++k) {
+      const float keep = b3 ? v[k + N / 8] : v[k], give = b3 ? v[k] : v[k + N / 8];
+      v[k] = keep + dpp<DPP_ROR8>(give);
+    }
+  }
+  // bit 2 (lane ^ 7 within an 8-lane group)
+  if (n > 1) {
+    n >>= 1;
+#pragma unroll
+    for (int k = 0; k < N / 16; ++k) {
+      const float keep = b2 ? v[k + N / 16] : v[k], give = b2 ? v[k] : v[k + N / 16];
+      v[k] = keep + dpp<DPP_HALF_MIRROR>(give);
+    }
+  }
+  // plain sums over the lane bits not used above: quads, then the rest
+  float x = v[0];
+  x += dpp<DPP_XOR1>(x);
+  x += dpp<DPP_XOR2>(x);
+  if (N < 16) x += dpp<DPP_HALF_MIRROR>(x);
+  if (N < 8) x += dpp<DPP_ROR8>(x);
+  return x;
+}
 
 // Sum over the 64 lanes, returned in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -265,12 +416,8 @@ __device__ __forceinline__ void rmsnorm2048(u32x4 (&xs)[4], const uint16_t* gamm
     const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float a = rbf(bf_lo(w[j]) * inv), b = rbf(bf_hi(w[j]) * inv);
-      if (gamma) {
-        a = bf_lo(g[j]) * a;
-        b = bf_hi(g[j]) * b;
-      }
-      w[j] = pack_bf2(a, b);
+      const uint32_t n = cvt_bf2(bf_lo(w[j]) * inv, bf_hi(w[j]) * inv);
+      w[j] = gamma ? cvt_bf2(bf_lo(g[j]) * bf_lo(n), bf_hi(g[j]) * bf_hi(n)) : n;
     }
     xs[i] = u32x4{w[0], w[1], w[2], w[3]};
   }
@@ -290,6 +437,7 @@ struct AttnShared {
   float pv[NWAVE][8][GQA * 8];
 };
 
+// rrow: the position's row of the RoPE table, bf16 cos[64] | sin[64].
 __device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rrow, int d) {
   // out[d]    = bf16(bf16(a*cos[d])    + bf16(-b*sin[d]))
   // out[d+32] = bf16(bf16(b*cos[d+32]) + bf16( a*sin[d+32]))      (attention.py:160-174)
@@ -357,17 +505,15 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  constexpr int R = ATT_R;
-  auto consume = [&](const u32x4(&kk)[R], const u32x4(&vv)[R], const bool(&valid)[R]) {
+  // consume rounds of 32 rows (R = rounds in the arrays): online softmax update
+  auto consume = [&](const auto& kk, const auto& vv, const auto& valid) {
+    constexpr int R = sizeof(valid) / sizeof(valid[0]);
     float sc[R][GQA];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int g = 0; g < GQA; ++g) {
-        float x = dot8(kk[r], q[g], 0.f);
-        x += __shfl_xor(x, 1, 64);
-        x += __shfl_xor(x, 2, 64);
-        x += __shfl_xor(x, 4, 64);
+        const float x = sum_lanes8(dot8(kk[r], q[g], 0.f));
         sc[r][g] = valid[r] ? x * SM_SCALE : -INFINITY;
       }
 #pragma unroll
@@ -403,24 +549,17 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     consume(A.k, A.v, A.valid);
     if (more) A = B;
   }
-  if (fresh) {   // the new row: row-lane 0 of the first round
-    u32x4 kk[R], vv[R];
-    bool valid[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      valid[r] = r == 0 && rl == 0;
-      kk[r] = valid[r] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-      vv[r] = valid[r] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + HD + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
+  if (fresh) {   // the new row: row-lane 0 of one round
+    const bool valid[1] = {rl == 0};
+    const u32x4 kk[1] = {valid[0] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + ch * 8) : u32x4{0u, 0u, 0u, 0u}};
+    const u32x4 vv[1] = {valid[0] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + HD + ch * 8)
+                                  : u32x4{0u, 0u, 0u, 0u}};
     consume(kk, vv, valid);
   }
   // merge the 32 row-lanes of the item: max, rescale, sum (lanes of one row agree)
 #pragma unroll
   for (int g = 0; g < GQA; ++g) {
-    float m = m_run[g];
-    m = fmaxf(m, __shfl_xor(m, 8, 64));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const float m = max_stride8(m_run[g]);
     if (lane == 0) sh.mx[wave][g] = m;
   }
   __syncthreads();
@@ -428,19 +567,10 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
   for (int g = 0; g < GQA; ++g) {
     const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
     const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
-    float l = l_run[g] * f;
-    l += __shfl_xor(l, 8, 64);
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = sum_stride8(l_run[g] * f);
     if (lane == 0) sh.sm[wave][g] = l;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc[g][e] * f;
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      acc[g][e] = v;
-    }
+    for (int e = 0; e < 8; ++e) acc[g][e] = sum_stride8(acc[g][e] * f);
   }
   if (lane < 8) {
 #pragma unroll

@@ -153,6 +153,13 @@ struct RowStream {
 #pragma unroll
     for (int j = 0; j < RING; ++j) issue(j, buf[j]);
   }
+  // When n <= RING: the per-lane partials of all RING slots (rows >= n read
+  // zero, so their partials are 0), with no refill loads.
+  template <class DotF, class T>
+  __device__ __forceinline__ void dots(DotF&& dotf, T (&part)[RING]) const {
+#pragma unroll
+    for (int j = 0; j < RING; ++j) part[j] = dotf(buf[j]);
+  }
   // dotf(buf) -> partial (per lane); emit(r, partial) for each valid row r.
   template <class DotF, class EmitF>
   __device__ __forceinline__ void run(DotF&& dotf, EmitF&& emit) {
@@ -234,6 +241,7 @@ struct Lds {
   __attribute__((aligned(16))) uint16_t v[INTER];   // staged GEMV input: attention output / act
   __attribute__((aligned(16))) uint16_t q[GQA * HD + 2 * HD];  // attention: 4 q heads | fresh k | fresh v
   float val[128];                                    // QKV dot products of this workgroup
+  __attribute__((aligned(16))) uint16_t rope[2 * HD];  // RoPE row of this step's position: cos | sin
   AttnShared att;
   float best[NWAVE];
   int bidx[NWAVE];
@@ -294,13 +302,21 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   u32x4 xs[4];
   lds_x2048(L.x, xs);
   rmsnorm2048(xs, nullptr);
-  auto emit = [&](int r, float part) {
-    const float v = wave_sum(part);
-    if (lane_id() == 0) L.val[wave + NWAVE * r] = v;
-  };
-  rs.run([&](const u32x4(&wv)[4]) { return dot2048(wv, xs); }, emit);
+  auto dotf = [&](const u32x4(&wv)[4]) { return dot2048(wv, xs); };
+  if (wn <= 4) {   // all rows in the ring: one transposed reduction
+    float pt[4];
+    rs.dots(dotf, pt);
+    const float v = reduce_rows<4>(pt);
+    const int r = lane_id() >> 4;
+    if ((lane_id() & 15) == 0 && r < wn) L.val[wave + NWAVE * r] = v;
+  } else {
+    rs.run(dotf, [&](int r, float part) {
+      const float v = wave_sum(part);
+      if (lane_id() == 0) L.val[wave + NWAVE * r] = v;
+    });
+  }
   __syncthreads();
-  const uint16_t* rrow = p.rope + (size_t)c.pos * (2 * HD);
+  const uint16_t* rrow = L.rope;
   uint16_t* xq = c.xb(li, X_QKV);
   for (int lp = threadIdx.x; lp < P1 - P0; lp += NT) {
     const int pr = P0 + lp, d = pr & 31;
@@ -398,6 +414,10 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     c.x_in = p.embed + (size_t)tok * H;
   }
   const int G = c.G, w = c.w, wave = wave_id(), lane = lane_id();
+  if (pos_ok && threadIdx.x < HD)   // the step's RoPE row, read once
+    reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] =
+        reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
+  __syncthreads();
 
   if (pos_ok) {
     int R0, R1;
@@ -428,13 +448,21 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         u32x4 xs[4];
         lds_x2048(L.v, xs);
         uint16_t* h1 = c.xb(li, X_H1);
-        float mine = 0.f;   // lane r: the wave's row r
-        os.run([&](const u32x4(&wv)[4]) { return dot2048(wv, xs); },
-               [&](int r, float part) {
-                 const float v = wave_sum(part);
-                 if (lane == r) mine = v;
-               });
-        if (lane < sp.n) st_dev(h1 + sp.lo + lane, f2bf(bf2f(L.x[sp.lo + lane]) + rbf(mine)));
+        auto dotf = [&](const u32x4(&wv)[4]) { return dot2048(wv, xs); };
+        if (sp.n <= 2) {   // lanes 0-31: row 0, lanes 32-63: row 1
+          float pt[2];
+          os.dots(dotf, pt);
+          const float v = reduce_rows<2>(pt);
+          const int r = lane >> 5;
+          if ((lane & 31) == 0 && r < sp.n) st_dev(h1 + sp.lo + r, f2bf(bf2f(L.x[sp.lo + r]) + rbf(v)));
+        } else {
+          float mine = 0.f;   // lane r: the wave's row r
+          os.run(dotf, [&](int r, float part) {
+            const float v = wave_sum(part);
+            if (lane == r) mine = v;
+          });
+          if (lane < sp.n) st_dev(h1 + sp.lo + lane, f2bf(bf2f(L.x[sp.lo + lane]) + rbf(mine)));
+        }
       }
 
       // ---- gate/up + SwiGLU -> act ----
@@ -471,17 +499,40 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           if (lane == r) mine = gv / (1.0f + __expf(-gv)) * uv;
         };
         wait_mem();   // this wave's LDS copy (and the ring) have landed
-        {
-          const uint8_t* src = L.gu[wave];
+        const uint8_t* src = L.gu[wave];
+        if (n_lds == GU_LDS_PAIRS && sp.n - n_lds <= 4) {
+          // 8 pairs: 16 rows (g of pairs 0-7, then u) in one transposed reduction
+          float pt[16];
+#pragma unroll
+          for (int j = 0; j < GU_LDS_PAIRS; ++j) {
+            u32x4 wv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
+            const GU2 d = gu_dot(wv);
+            pt[j] = d.g;
+            pt[8 + j] = d.u;
+          }
+          GU2 rp[4];
+          gs.dots(gu_dot, rp);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            pt[GU_LDS_PAIRS + j] = rp[j].g;
+            pt[8 + GU_LDS_PAIRS + j] = rp[j].u;
+          }
+          const float v = reduce_rows<16>(pt);   // lane 4k..4k+3: row k
+          const Pair gu = xor32_pair(v);         // lanes 0-31: g (own) and u (lane + 32)
+          const int r = lane >> 2;
+          if (lane < 32 && (lane & 3) == 0 && r < sp.n) st_dev(act + sp.lo + r, f2bf(gu.a / (1.0f + __expf(-gu.a)) * gu.b));
+        } else {
           for (int j = 0; j < n_lds; ++j) {
             u32x4 wv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
             gu_emit(j, gu_dot(wv));
           }
+          gs.run(gu_dot, [&](int r, GU2 part) { gu_emit(n_lds + r, part); });
+          if (lane < sp.n) st_dev(act + sp.lo + lane, f2bf(mine));
         }
-        gs.run(gu_dot, [&](int r, GU2 part) { gu_emit(n_lds + r, part); });
-        if (lane < sp.n) st_dev(act + sp.lo + lane, f2bf(mine));
       }
 
       // ---- down projection + residual -> h2 ----
@@ -498,25 +549,34 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         u32x4 xs[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) xs[i] = *reinterpret_cast<const u32x4*>(L.v + i * 512 + lane * 8);
-        float mine = 0.f;   // lane r: the wave's row r
-        ds.run([&](const u32x4(&wv)[16]) {
-                 float a = 0.f, b = 0.f;
+        auto dotf = [&](const u32x4(&wv)[16]) {
+          float a = 0.f, b = 0.f;
 #pragma unroll
-                 for (int i = 0; i < 16; i += 2) {
-                   a = dot8(wv[i], xs[i], a);
-                   b = dot8(wv[i + 1], xs[i + 1], b);
-                 }
-                 return a + b;
-               },
-               [&](int r, float part) {
-                 const float v = wave_sum(part);
-                 if (lane == r) mine = v;
-               });
-        if (lane < sp.n) {
-          const int row = sp.lo + lane;
-          const uint32_t hv = f2bf(bf2f(L.h1[row]) + rbf(mine));
+          for (int i = 0; i < 16; i += 2) {
+            a = dot8(wv[i], xs[i], a);
+            b = dot8(wv[i + 1], xs[i + 1], b);
+          }
+          return a + b;
+        };
+        auto out = [&](int r, float v) {
+          const int row = sp.lo + r;
+          const uint32_t hv = f2bf(bf2f(L.h1[row]) + rbf(v));
           st_dev(h2 + row, hv);
           if (last && p.hidden_out) p.hidden_out[row] = (uint16_t)hv;
+        };
+        if (sp.n <= 2) {   // lanes 0-31: row 0, lanes 32-63: row 1
+          float pt[2];
+          ds.dots(dotf, pt);
+          const float v = reduce_rows<2>(pt);
+          const int r = lane >> 5;
+          if ((lane & 31) == 0 && r < sp.n) out(r, v);
+        } else {
+          float mine = 0.f;   // lane r: the wave's row r
+          ds.run(dotf, [&](int r, float part) {
+            const float v = wave_sum(part);
+            if (lane == r) mine = v;
+          });
+          if (lane < sp.n) out(lane, mine);
         }
       }
     }
