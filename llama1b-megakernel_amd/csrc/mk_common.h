@@ -240,6 +240,37 @@ __device__ __forceinline__ float reduce_rows(const float (&in)[N]) {
   return x;
 }
 
+// In-place sum (or max) of N = 4 or 32 per-lane values over the 8 lanes that
+// share lane & 7 (lane bits 3-5), transposed like reduce_rows: afterwards
+// v[0 .. N/8) of lane i hold values (4*b5 + 2*b4 + b3) * N/8 + k of the
+// original array (for N = 4: v[0] holds value 2*b5 + b4).
+template <int N, bool MAX>
+__device__ __forceinline__ void reduce_stride8(float (&v)[N]) {
+  static_assert(N == 4 || N == 32, "4 or 32 values");
+  const int lane = threadIdx.x & 63;
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const Pair p = swap32(v[k], v[k + N / 2]);
+    v[k] = op(p.a, p.b);
+  }
+#pragma unroll
+  for (int k = 0; k < N / 4; ++k) {
+    const Pair p = swap16(v[k], v[k + N / 4]);
+    v[k] = op(p.a, p.b);
+  }
+  if (N == 4) {
+    v[0] = op(v[0], dpp<DPP_ROR8>(v[0]));
+  } else {
+    const bool b3 = lane & 8;
+#pragma unroll
+    for (int k = 0; k < N / 8; ++k) {
+      const float keep = b3 ? v[k + N / 8] : v[k], give = b3 ? v[k] : v[k + N / 8];
+      v[k] = op(keep, dpp<DPP_ROR8>(give));
+    }
+  }
+}
+
 // Sum over the 64 lanes, returned in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<DPP_XOR1>(v);
@@ -505,16 +536,20 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  // consume rounds of 32 rows (R = rounds in the arrays): online softmax update
-  auto consume = [&](const auto& kk, const auto& vv, const auto& valid) {
+  // consume rounds of 32 rows (R = rounds in the arrays, the first nr of them
+  // holding any valid row): online softmax update
+  auto consume = [&](const auto& kk, const auto& vv, const auto& valid, int nr) {
     constexpr int R = sizeof(valid) / sizeof(valid[0]);
     float sc[R][GQA];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int g = 0; g < GQA; ++g) {
-        const float x = sum_lanes8(dot8(kk[r], q[g], 0.f));
-        sc[r][g] = valid[r] ? x * SM_SCALE : -INFINITY;
+        sc[r][g] = -INFINITY;
+        if (r < nr) {
+          const float x = sum_lanes8(dot8(kk[r], q[g], 0.f));
+          sc[r][g] = valid[r] ? x * SM_SCALE : -INFINITY;
+        }
       }
 #pragma unroll
     for (int g = 0; g < GQA; ++g) {
@@ -527,6 +562,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
       for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
+        if (r >= nr) continue;
         const float pr = valid[r] ? __expf(sc[r][g] - mn) : 0.f;
         l_run[g] += pr;
         const uint32_t w4[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
@@ -546,7 +582,8 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     AttnGroup B;
     const bool more = gi + 1 < ngroups;
     if (more) rows.load(gi + 1, B);
-    consume(A.k, A.v, A.valid);
+    const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
+    consume(A.k, A.v, A.valid, left >= ATT_GROUP ? ATT_R : (left + 31) / 32);
     if (more) A = B;
   }
   if (fresh) {   // the new row: row-lane 0 of one round
@@ -554,29 +591,32 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     const u32x4 kk[1] = {valid[0] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + ch * 8) : u32x4{0u, 0u, 0u, 0u}};
     const u32x4 vv[1] = {valid[0] ? *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + HD + ch * 8)
                                   : u32x4{0u, 0u, 0u, 0u}};
-    consume(kk, vv, valid);
+    consume(kk, vv, valid, 1);
   }
-  // merge the 32 row-lanes of the item: max, rescale, sum (lanes of one row agree)
+  // merge the 32 row-lanes of the item (lane bits 3-5 within a wave, then the
+  // 4 waves through LDS): max, rescale, sum. The lanes of one row agree.
+  {
+    float mv[GQA];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) {
-    const float m = max_stride8(m_run[g]);
-    if (lane == 0) sh.mx[wave][g] = m;
+    for (int g = 0; g < GQA; ++g) mv[g] = m_run[g];
+    reduce_stride8<GQA, true>(mv);   // lane: head 2*b5 + b4
+    if ((lane & 15) == 0) sh.mx[wave][lane >> 4] = mv[0];
   }
   __syncthreads();
+  {
+    float lv[GQA], av[GQA * 8];
 #pragma unroll
-  for (int g = 0; g < GQA; ++g) {
-    const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
-    const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
-    const float l = sum_stride8(l_run[g] * f);
-    if (lane == 0) sh.sm[wave][g] = l;
+    for (int g = 0; g < GQA; ++g) {
+      const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
+      const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
+      lv[g] = l_run[g] * f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = sum_stride8(acc[g][e] * f);
-  }
-  if (lane < 8) {
-#pragma unroll
-    for (int g = 0; g < GQA; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sh.pv[wave][ch][g * 8 + e] = acc[g][e];
+      for (int e = 0; e < 8; ++e) av[g * 8 + e] = acc[g][e] * f;
+    }
+    reduce_stride8<GQA, false>(lv);       // lane: head 2*b5 + b4
+    if ((lane & 15) == 0) sh.sm[wave][lane >> 4] = lv[0];
+    reduce_stride8<GQA * 8, false>(av);   // lane: values 4*(lane >> 3) .. +3 of head-major [4][8]
+    *reinterpret_cast<float4*>(&sh.pv[wave][ch][(lane >> 3) * 4]) = make_float4(av[0], av[1], av[2], av[3]);
   }
   __syncthreads();
   {
