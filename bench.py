@@ -2,8 +2,9 @@
 """Benchmark: bs=1 Llama-3.2-1B decode on one MI355X (BASELINE.json metric).
 
 Workload ("C3"): random-init bf16 weights (seed 0),
-a 384-token uniform-random prompt prefilled into a 1024-row KV cache by the
-megakernel itself, then greedy decode. A *step* is one decode step — one
+a 384-token uniform-random prompt prefilled into a 1024-row KV cache on the
+GPU (the batched kernel's prefill step, 32 prompt tokens per launch; its
+latency is reported as prefill_ms), then greedy decode. A *step* is one decode step — one
 launch of the persistent megakernel (16 layers + final norm + tied lm_head +
 argmax) for one token; the token and position are fed back on the device, so
 consecutive steps need no host work. W untimed warm-up steps run first, the
@@ -135,7 +136,14 @@ def main():
     log(f"[bench] weights packed in {time.perf_counter() - t0:.1f}s; grid = {mk_lib.load().mk_grid_size(0)} WGs")
 
     prompt = random_token_ids(PROMPT, seed=0)
-    model.prefill(prompt)
+    model.prefill(prompt)                        # warm-up (first use allocates the prefill workspace)
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    model.prefill(prompt)                        # context encoding: 383 prompt tokens in chunks of 32
+    torch.cuda.synchronize()
+    prefill_ms = (time.perf_counter() - tp) * 1e3
+    if model.prefill_device_error():
+        sys.exit("device error in the prefill steps")
     dec = model.launcher("decode")
     dec.launch()                                 # position 383 -> first generated token
     torch.cuda.synchronize()
@@ -181,6 +189,7 @@ def main():
         "ms_per_step": round(wall * 1e3 / K, 4),
         "p50_step_ms": round(statistics.median(step_ms), 4),
         "p90_step_ms": round(sorted(step_ms)[int(0.9 * (K - 1))], 4),
+        "prefill_ms": round(prefill_ms, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -59,6 +59,15 @@ extern "C" {
                                       one-workgroup-per-CU grid guaranteed by the
                                       runtime (default: a plain launch, which
                                       leaves ~20 us less between steps)          */
+#define MK_FLAG_PREFILL      0x4u  /* context encoding: the batch's tokens are
+                                      consecutive tokens of ONE sequence, token b
+                                      at position pos[b] = pos[0] + b, all using
+                                      sequence 0 of the caches (k_cache[l] may be
+                                      [1][8][s_max][64]); token b attends to rows
+                                      [0, pos[b]], including the rows the other
+                                      tokens of the step write. Needs a batched
+                                      workspace (mk_workspace_bytes(batch >= 2)). */
+#define MK_DEVERR_PREFILL    0x4u  /* MK_FLAG_PREFILL with pos[b] != pos[0] + b: step skipped */
 
 /* Model constants the kernel is built for (Llama-3.2-1B). */
 #define MK_HIDDEN      2048

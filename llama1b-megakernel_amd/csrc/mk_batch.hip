@@ -122,6 +122,8 @@ struct BCtx {
   const BParams* p;
   Sync s;
   int G, w, B;
+  bool prefill;     // MK_FLAG_PREFILL: every token uses sequence 0 of the caches
+  __device__ __forceinline__ int cache_seq(int b) const { return prefill ? 0 : b; }
   uint8_t* hcnt;    // this launch's hand-over counters [layer][5][8 lines]
   uint32_t* acnt;   // this launch's attention-split counters [layer][M][8]
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
@@ -370,9 +372,10 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
           const bool is_k = pr < Q_PAIRS + K_PAIRS;
           const int kh = (pr - Q_PAIRS - (is_k ? 0 : K_PAIRS)) >> 5;
           col = NQ * HD + (is_k ? 0 : NKV * HD) + kh * HD + dd + 32 * hi;
-          // the cache row is read only by later launches: a plain store
-          uint16_t* crow = (is_k ? p.kc[li] : p.vc[li]) + ((size_t)(m * NKV + kh) * p.s_max + ps) * HD + dd + 32 * hi;
-          *crow = (uint16_t)outv;
+          // device scope: in a prefill step the other tokens' attention reads this row
+          uint16_t* crow =
+              (is_k ? p.kc[li] : p.vc[li]) + ((size_t)(c.cache_seq(m) * NKV + kh) * p.s_max + ps) * HD + dd + 32 * hi;
+          st_dev(crow, outv);
         }
         st_dev(xq + (size_t)m * QKV_ROWS + col, outv);
       }
@@ -399,11 +402,12 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     const int j0 = sp * rows, j1 = min(j0 + rows, ps + 1);
     const bool fresh = ps >= j0 && ps < j1;
     // the item's cached rows do not depend on this step: their first group is issued before the wait for q
-    const size_t head = (size_t)(b * NKV + h) * p.s_max * HD;
+    // (in a prefill step rows of this step's tokens are among them: issued after the wait)
+    const size_t head = (size_t)(c.cache_seq(b) * NKV + h) * p.s_max * HD;
     AttnRows ar;
     ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
     AttnGroup g0;
-    ar.load(0, g0);
+    if (!c.prefill) ar.load(0, g0);
     if (wave_id() == 0) {
       if (!waited) {
         trace_mark(c.s, 2 * xk(li, 2) - 1);
@@ -421,6 +425,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     }
     waited = true;
     __syncthreads();
+    if (c.prefill) ar.load(0, g0);
     attn_item(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
     // publish the partial and count it in; the last arrival merges
     wait_mem();
@@ -707,6 +712,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.G = gridDim.x;
   c.w = blockIdx.x;
   c.B = p.batch;
+  c.prefill = (p.flags & MK_FLAG_PREFILL) != 0;
   const int t = threadIdx.x;
   const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const size_t cset = bws_cnt_set(p.max_batch);
@@ -726,13 +732,17 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
   }
   __syncthreads();
-  bool pos_ok = true;
+  bool pos_ok = true, run_ok = true;
   for (int b = 0; b < c.B; ++b) {
     const int ps = L.pos[b];
     pos_ok = pos_ok && ps >= 0 && ps < p.s_max && ps < p.rope_rows;
+    run_ok = run_ok && (!c.prefill || ps == L.pos[0] + b);
   }
   if (!pos_ok && blockIdx.x == 0 && t == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!run_ok && blockIdx.x == 0 && t == 0)
+    __hip_atomic_fetch_or(c.s.err, MK_DEVERR_PREFILL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  pos_ok = pos_ok && run_ok;
   if (pos_ok && t == 0) {
     // attention items: about two per workgroup over all sequences' KV rows
     long long total = 0;

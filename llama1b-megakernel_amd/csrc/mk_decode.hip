@@ -892,6 +892,8 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   if (a->batch > xe.max_batch)
     return fail(MK_ERR_WORKSPACE, "batch %d exceeds the workspace's batch %d (mk_workspace_bytes)", a->batch,
                 xe.max_batch);
+  if ((a->flags & MK_FLAG_PREFILL) && xe.max_batch == 1)
+    return fail(MK_ERR_UNSUPPORTED, "MK_FLAG_PREFILL needs a batched workspace (mk_workspace_bytes with batch >= 2)");
   if (xe.max_batch > 1) {
     // batched layout: MFMA kernel (mk_batch.hip) for every batch size on this workspace
     if (a->workspace_bytes < batch_ws_bytes(xe.max_batch))

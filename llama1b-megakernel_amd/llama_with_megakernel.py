@@ -20,9 +20,12 @@ Mirrors the reference module ``llama_with_megakernel`` (selected by
 
 ``model_path`` is a local HF checkpoint directory (safetensors) or
 ``"random:<seed>"`` for the synthetic N(0, 0.02) weights used by the
-benchmarks. Prefill runs the megakernel once per prompt token (the same
-decode step with logits skipped), so the KV cache is produced by the same
-kernel that decodes.
+benchmarks. Prefill (context encoding, the reference's baseline-layer path at
+llama_with_megakernel.py:194-204) runs the batched MFMA kernel over chunks of
+up to 32 consecutive prompt tokens per launch (``MK_FLAG_PREFILL``: causal
+attention over the cache rows, including the rows of the chunk's own earlier
+tokens); ``prefill(..., batched=False)`` instead runs the decode megakernel
+once per prompt token with logits skipped.
 
 TP must be 1, as the reference asserts (llama_with_megakernel.py:147-150).
 """
@@ -133,6 +136,8 @@ class NeuronLlamaForCausalLMMK:
         self.tokens = torch.zeros(nc.batch_size, dtype=torch.int32, device=dev)
         self.logits = torch.zeros(nc.batch_size, d.vocab, dtype=torch.float32, device=dev)
         self.hidden_out = torch.zeros(nc.batch_size, d.hidden, dtype=torch.bfloat16, device=dev)
+        self.pf_ws: Optional[mk_lib.Workspace] = None   # batched workspace of the prefill steps (on first use)
+        self.pf_pos = torch.arange(self.s_max, dtype=torch.int32, device=dev)
         self._ready = True
         self._launchers: Dict[str, mk_lib.StepLauncher] = {}
 
@@ -186,17 +191,36 @@ class NeuronLlamaForCausalLMMK:
         return self.logits, kv
 
     @torch.no_grad()
-    def prefill(self, prompt: torch.Tensor) -> None:
-        """Write the prompt's K/V (positions 0..n-1); leaves the last prompt
-        token in the token buffer and pos = n - 1."""
+    def prefill(self, prompt: torch.Tensor, batched: bool = True) -> None:
+        """Write the K/V rows of prompt tokens 0..n-2 (positions 0..n-2); leaves
+        the last prompt token in the token buffer and pos = n - 1, so the next
+        decode step processes it and yields the first generated token.
+
+        batched: chunks of up to 32 tokens per launch of the batched kernel
+        (MK_FLAG_PREFILL); otherwise one decode-kernel launch per token."""
         self.reset()
         n = int(prompt.numel())
+        if n < 1 or n > self.s_max:
+            raise ValueError(f"prompt of {n} tokens does not fit max_context_length {self.s_max}")
         prompt_dev = prompt.reshape(-1).to(device=self.pos.device, dtype=torch.int32)
-        pf = self.launcher("prefill")
-        for i in range(n - 1):
-            self.tokens.copy_(prompt_dev[i:i + 1])
-            pf.launch()
+        if batched:
+            if self.pf_ws is None:
+                self.pf_ws = mk_lib.Workspace(mk_lib.PREFILL_CHUNK, self.s_max, self.pos.device)
+            for c0 in range(0, n - 1, mk_lib.PREFILL_CHUNK):
+                m = min(mk_lib.PREFILL_CHUNK, n - 1 - c0)
+                mk_lib.decode_step(self.weights, self.pf_ws, self.k_caches, self.v_caches, self.pf_pos[c0:c0 + m],
+                                   tokens=prompt_dev[c0:c0 + m], flags=mk_lib.MK_FLAG_PREFILL, batch=m)
+            self.pos.fill_(n - 1)
+        else:
+            pf = self.launcher("prefill")
+            for i in range(n - 1):
+                self.tokens.copy_(prompt_dev[i:i + 1])
+                pf.launch()
         self.tokens.copy_(prompt_dev[n - 1:n])
+
+    def prefill_device_error(self) -> int:
+        """Device error bits of the prefill steps since the last call (0 = none)."""
+        return 0 if self.pf_ws is None else self.pf_ws.read_device_error()
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, return_logits: bool = False):
@@ -216,7 +240,7 @@ class NeuronLlamaForCausalLMMK:
             if return_logits:
                 logits.append(self.logits.clone())
         torch.cuda.synchronize()
-        bits = self.ws.read_device_error()
+        bits = self.ws.read_device_error() | self.prefill_device_error()
         if bits:
             raise RuntimeError(f"megakernel device error bits 0x{bits:x}")
         if return_logits:

@@ -25,8 +25,11 @@ ERRORS = {
 MK_DEVERR_POS = 0x1
 MK_DEVERR_SYNC = 0x2
 MK_DEVERR_BARRIER = MK_DEVERR_SYNC
+MK_DEVERR_PREFILL = 0x4
 MK_FLAG_ADVANCE = 0x1
 MK_FLAG_COOPERATIVE = 0x2
+MK_FLAG_PREFILL = 0x4
+PREFILL_CHUNK = 32          # tokens per prefill step (the batched kernel's largest batch)
 
 HIDDEN, N_KV, HEAD_DIM, VOCAB, MAX_LAYERS = 2048, 8, 64, 128256, 16
 
