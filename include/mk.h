@@ -160,6 +160,43 @@ typedef struct mk_step_args {
 
 #define MK_TRACE_SLOTS 256
 
+/*
+ * On-device sampling of the next token from fp32 logits (after a decode step
+ * that wrote `logits`). Counterpart of NxDI's on-device sampler configured by
+ * --top-k / --top-p / --temperature / --global-topk / --on-device-sampling
+ * (main.py:57-61, 85, 129-130) with per-sequence sampling parameters as built
+ * by prepare_sampling_params (main.py:195-206).
+ *   params: device fp32 [batch][3] = (top_k, top_p, temperature) per row.
+ *     top_k == 1 or temperature <= 0: greedy argmax (lowest index on ties);
+ *     top_k <= 0 or > MK_SAMPLE_MAX_TOPK: the global cap MK_SAMPLE_MAX_TOPK;
+ *     tokens with logit/temperature >= the top_k-th largest are kept (ties
+ *     included, at most MK_SAMPLE_CAND of them), then top_p in (0, 1) keeps,
+ *     in descending order, each token whose preceding softmax mass is < top_p;
+ *     one draw from the renormalised kept distribution (inverse CDF in
+ *     descending order) with u = Philox4x32-10(key = seed, counter =
+ *     (counter[row], row, 0, 0)) first word >> 8, times 2^-24.
+ *   counter: device int32 [batch] (e.g. the sequences' positions) or NULL (0).
+ *   tokens_out: device int32 [batch]; uniforms_out: device fp32 [batch] (the u
+ *     each row used, -1 for greedy rows) or NULL.
+ * Asynchronous on `stream`; allocates nothing.
+ */
+#define MK_SAMPLE_MAX_TOPK 1024
+#define MK_SAMPLE_CAND     2048
+typedef struct mk_sample_args {
+    const float *logits;
+    int32_t batch;
+    int32_t vocab;
+    int32_t vocab_stride;      /* floats between rows of logits (>= vocab) */
+    const float *params;
+    uint64_t seed;
+    const int32_t *counter;
+    int32_t *tokens_out;
+    float *uniforms_out;
+    void *stream;
+} mk_sample_args;
+int mk_sample(const mk_sample_args *a);
+const char *mk_sample_last_error(void);
+
 /* Library / device information. */
 int mk_abi_version(void);
 const char *mk_last_error(void);

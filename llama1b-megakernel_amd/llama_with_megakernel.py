@@ -162,6 +162,9 @@ class NeuronLlamaForCausalLMMK:
             elif kind == "decode":
                 l = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, logits=self.logits,
                                         next_token=self.tokens, hidden_out=self.hidden_out, **common)
+            elif kind == "decode_logits":   # logits only: the next token comes from mk_sample
+                l = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, logits=self.logits,
+                                        hidden_out=self.hidden_out, **common)
             else:
                 raise ValueError(kind)
             self._launchers[kind] = l
@@ -223,19 +226,59 @@ class NeuronLlamaForCausalLMMK:
         return 0 if self.pf_ws is None else self.pf_ws.read_device_error()
 
     @torch.no_grad()
-    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, return_logits: bool = False):
-        """Greedy generation for one sequence: returns the new token ids
-        (and the per-step fp32 logits if requested)."""
+    def decode_graph(self, n_steps: int, sampling_params: Optional[torch.Tensor] = None, seed: int = 0):
+        """Capture ``n_steps`` consecutive decode steps (each followed by the
+        on-device sampler if ``sampling_params`` is given) into one HIP graph.
+
+        Every step reads its token and position from the device and writes
+        them back (MK_FLAG_ADVANCE), so a replay continues from whatever state
+        the model is in — e.g. right after ``prefill`` — exactly as the same
+        launches issued one by one; the step's token is also appended to
+        ``self.graph_tokens[:n_steps]``. The graph runs on a private stream;
+        ``replay()`` orders it after the current stream's work."""
+        if sampling_params is not None:
+            sampling_params = sampling_params.to(device=self.pos.device, dtype=torch.float32).reshape(1, 3)
+        stream = torch.cuda.Stream(device=self.pos.device)
+        kw = dict(pos=self.pos, tokens=self.tokens, flags=mk_lib.MK_FLAG_ADVANCE, logits=self.logits,
+                  hidden_out=self.hidden_out, stream=stream)
+        if sampling_params is None:
+            kw["next_token"] = self.tokens
+        step = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, **kw)
+        self.graph_tokens = torch.zeros(n_steps, dtype=torch.int32, device=self.pos.device)
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n_steps):
+                step.launch()
+                if sampling_params is not None:
+                    mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
+                self.graph_tokens[i:i + 1].copy_(self.tokens)
+        graph._mk_keep = (step, sampling_params, stream)
+        return graph
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, return_logits: bool = False,
+                 sampling_params: Optional[torch.Tensor] = None, seed: int = 0):
+        """Generation for one sequence: returns the new token ids (and the
+        per-step fp32 logits if requested). Greedy (the decode kernel's argmax)
+        unless ``sampling_params`` [1, 3] (top_k, top_p, temperature) is given:
+        then each step's logits go through the on-device sampler, whose Philox
+        counter is the position of the token being produced (reproducible for
+        a given seed)."""
         prompt = input_ids.reshape(-1)
         n = int(prompt.numel())
         if n + max_new_tokens - 1 > self.s_max:
             raise ValueError(f"{n} + {max_new_tokens} tokens exceed max_context_length {self.s_max}")
         self.prefill(prompt)
-        dec = self.launcher("decode")
+        dec = self.launcher("decode" if sampling_params is None else "decode_logits")
+        if sampling_params is not None:
+            sampling_params = sampling_params.to(device=self.pos.device, dtype=torch.float32).reshape(1, 3)
         out = torch.empty(max_new_tokens, dtype=torch.int32, device=self.pos.device)
         logits = [] if return_logits else None
         for t in range(max_new_tokens):
             dec.launch()
+            if sampling_params is not None:
+                mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
             out[t:t + 1].copy_(self.tokens)
             if return_logits:
                 logits.append(self.logits.clone())

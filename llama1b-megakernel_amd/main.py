@@ -53,6 +53,15 @@ def parse_args(argv=None):
     ap.add_argument("--batch-size", type=int, default=1)
     ap.add_argument("--tp-degree", type=int, default=1)
     ap.add_argument("--top-k", type=int, default=1)
+    ap.add_argument("--top-p", type=float, default=1.0)
+    ap.add_argument("--temperature", type=float, default=1.0)
+    ap.add_argument("--global-topk", type=int, default=None,
+                    help="candidate cap of the on-device sampler (at most 1024, the built-in cap)")
+    ap.add_argument("--do-sample", type=lambda v: str(v).lower() in ("1", "true", "yes"), default=True)
+    ap.add_argument("--on-device-sampling", action="store_true",
+                    help="accepted for the reference's CLI; sampling always runs on the GPU here")
+    ap.add_argument("--seed", type=int, default=0, help="Philox key of the on-device sampler")
+    ap.add_argument("--graph", action="store_true", help="benchmark: replay the decode steps as one HIP graph")
     ap.add_argument("--num-runs", type=int, default=5)
     ap.add_argument("--num-tokens-to-check", type=int, default=None)
     return ap.parse_args(argv)
@@ -65,10 +74,22 @@ def prompt_ids(args):
     return random_token_ids(args.prompt_len, seed=0)
 
 
+def sampling_params(args):
+    """[1, 3] device tensor (top_k, top_p, temperature), or None for greedy
+    (top_k == 1 or do_sample false), as the reference's generation config."""
+    import mk_lib
+    if not args.do_sample or args.top_k == 1:
+        return None
+    if args.global_topk is not None and not 1 <= args.global_topk <= mk_lib.SAMPLE_MAX_TOPK:
+        raise SystemExit(f"--global-topk must be in [1, {mk_lib.SAMPLE_MAX_TOPK}]")
+    k = args.top_k
+    if args.global_topk is not None and (k <= 0 or k > args.global_topk):
+        k = args.global_topk
+    return mk_lib.prepare_sampling_params(1, k, args.top_p, args.temperature)
+
+
 def prepare_inference(args):
     from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
-    if args.top_k != 1:
-        raise SystemExit("only greedy decoding (top_k=1) is built")
     nc = NeuronConfigLlamaMK(batch_size=args.batch_size, seq_len=args.seq_len,
                              max_context_length=args.max_context_length or args.seq_len,
                              tp_degree=args.tp_degree)
@@ -92,8 +113,10 @@ def run_generation(args):
     ids = prompt_ids(args)
     if args.enable_nki:
         model = prepare_inference(args)
-        out = model.generate(ids, args.max_new_tokens)
+        out = model.generate(ids, args.max_new_tokens, sampling_params=sampling_params(args), seed=args.seed)
     else:
+        if sampling_params(args) is not None:
+            raise SystemExit("the stock path decodes greedily; sampling needs --enable-nki")
         from llama_baseline import StockLlama
         from mk_weights import load_hf_checkpoint, synthetic_state_dict
         sd = (synthetic_state_dict(int(args.model_path.split(":")[1] or 0)) if args.model_path.startswith("random:")
@@ -160,9 +183,18 @@ def overall_agreement_floor(n: int) -> float:
 
 
 def benchmark_sampling(args):
+    """The reference's benchmark_sampling / generate_report (main.py:178-271):
+    e2e, context encoding (prefill) and per-token generation latencies over
+    num_runs runs after one warm-up run. With --graph the token-generation
+    steps of a run replay one captured HIP graph (per-token latency is then
+    the run's generation time / tokens)."""
+    import mk_lib
     ids = prompt_ids(args)
     model = prepare_inference(args)
     n_new = args.max_new_tokens
+    sp = sampling_params(args)
+    dec = model.launcher("decode" if sp is None else "decode_logits")
+    graph = model.decode_graph(n_new, sampling_params=sp, seed=args.seed) if args.graph else None
     e2e, cte, tkg = [], [], []
     for r in range(args.num_runs + 1):
         torch.cuda.synchronize()
@@ -170,19 +202,28 @@ def benchmark_sampling(args):
         model.prefill(ids)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        dec = model.launcher("decode")
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_new + 1)]
-        ev[0].record()
-        for i in range(n_new):
-            dec.launch()
-            ev[i + 1].record()
+        if graph is not None:
+            ev[0].record()
+            graph.replay()
+            ev[n_new].record()
+        else:
+            ev[0].record()
+            for i in range(n_new):
+                dec.launch()
+                if sp is not None:
+                    mk_lib.sample(model.logits, sp, model.tokens, seed=args.seed, counter=model.pos)
+                ev[i + 1].record()
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         if r == 0:
             continue            # warm-up run
         e2e.append((t2 - t0) * 1e3)
         cte.append((t1 - t0) * 1e3)
-        tkg += [ev[i].elapsed_time(ev[i + 1]) for i in range(n_new)]
+        if graph is not None:
+            tkg += [ev[0].elapsed_time(ev[n_new]) / n_new] * n_new
+        else:
+            tkg += [ev[i].elapsed_time(ev[i + 1]) for i in range(n_new)]
 
     def rep(lat, tokens):
         lat_s = sorted(lat)

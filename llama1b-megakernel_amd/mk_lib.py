@@ -53,6 +53,17 @@ class MkStepArgs(ctypes.Structure):
     ]
 
 
+class MkSampleArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_void_p), ("batch", c_int32), ("vocab", c_int32), ("vocab_stride", c_int32),
+        ("params", c_void_p), ("seed", ctypes.c_uint64), ("counter", c_void_p), ("tokens_out", c_void_p),
+        ("uniforms_out", c_void_p), ("stream", c_void_p),
+    ]
+
+
+SAMPLE_MAX_TOPK = 1024
+
+
 class MkError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"{ERRORS.get(code, code)}: {msg}")
@@ -86,6 +97,9 @@ def load() -> ctypes.CDLL:
         lib.mk_layer_step.argtypes = [POINTER(MkWeights), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.mk_layer_step.restype = c_int
+        lib.mk_sample.argtypes = [POINTER(MkSampleArgs)]
+        lib.mk_sample.restype = c_int
+        lib.mk_sample_last_error.restype = c_char_p
         _lib = lib
     return _lib
 
@@ -155,6 +169,37 @@ def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tens
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes,
                    current_stream_ptr(), _ptr(trace))
     check(load().mk_decode_step(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def prepare_sampling_params(batch_size: int, top_k, top_p, temperature, device="cuda") -> torch.Tensor:
+    """Device fp32 [batch][3] rows (top_k, top_p, temperature); a single value
+    broadcasts (the tensor NxDI's prepare_sampling_params builds, main.py:195-206)."""
+    def col(v):
+        v = list(v) if isinstance(v, (list, tuple)) else [v]
+        return v * batch_size if len(v) == 1 else v
+    rows = list(zip(col(top_k), col(top_p), col(temperature)))
+    if len(rows) != batch_size:
+        raise ValueError(f"sampling parameters for {len(rows)} rows, batch {batch_size}")
+    return torch.tensor(rows, dtype=torch.float32, device=device)
+
+
+def sample(logits: torch.Tensor, params: torch.Tensor, tokens_out: torch.Tensor, *, seed: int = 0,
+           counter: Optional[torch.Tensor] = None, uniforms_out: Optional[torch.Tensor] = None) -> None:
+    """``mk_sample`` on the current stream: next tokens from fp32 logits [B, V]
+    with per-row (top_k, top_p, temperature); ``counter`` [B] int32 (e.g. the
+    positions) feeds the Philox counter."""
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be fp32 [B, V] with unit column stride")
+    B, V = logits.shape
+    if params.shape != (B, 3) or params.dtype != torch.float32 or not params.is_contiguous():
+        raise ValueError("params must be contiguous fp32 [B, 3]")
+    if tokens_out.dtype != torch.int32 or tokens_out.numel() < B:
+        raise ValueError("tokens_out must be int32 with at least B elements")
+    a = MkSampleArgs(logits.data_ptr(), B, V, logits.stride(0), params.data_ptr(), seed & 0xFFFFFFFFFFFFFFFF,
+                     _ptr(counter), tokens_out.data_ptr(), _ptr(uniforms_out), current_stream_ptr())
+    rc = load().mk_sample(ctypes.byref(a))
+    if rc != MK_OK:
+        raise MkError(rc, load().mk_sample_last_error().decode(errors="replace"))
 
 
 class StepLauncher:
