@@ -48,6 +48,10 @@
 #include "mk_batch.h"
 #include "mk_common.h"
 
+#ifndef MK_BATT_DEPTH
+#define MK_BATT_DEPTH 1
+#endif
+
 namespace {
 
 using namespace mk;
@@ -426,7 +430,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     waited = true;
     __syncthreads();
     if (c.prefill) ar.load(0, g0);
-    attn_item(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
+    attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
     // publish the partial and count it in; the last arrival merges
     wait_mem();
     __syncthreads();

@@ -520,8 +520,10 @@ struct AttnRows {
 // (the cached rows do not depend on the current step, so a caller issues them
 // before it waits for q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
 // Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
-// of it; rows stream in groups of ATT_GROUP with an online softmax. Writes
-// the item's partial (m[4], l[4], o[4][64]) unnormalised, relative to m.
+// of it; rows stream in groups of ATT_GROUP with an online softmax, DEPTH
+// (1 or 2) groups ahead in flight. Writes the item's partial (m[4], l[4],
+// o[4][64]) unnormalised, relative to m.
+template <int DEPTH = 1>
 __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first, const uint16_t* q_lds, bool fresh,
                                           float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
@@ -575,16 +577,34 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
       m_run[g] = mn;
     }
   };
-  // cached rows in groups of ATT_GROUP, the next group's loads in flight while one is consumed
+  // cached rows in groups of ATT_GROUP, the loads of the next DEPTH groups in flight while one is
+  // consumed. The buffers rotate by unrolling (a register copy of a buffer whose loads are in
+  // flight would wait for them), and the loads ahead are issued unconditionally (rows past the
+  // item read nothing: out-of-range offsets), so the compiler's wait before each consume counts
+  // exactly the loads issued after it instead of falling back to waiting for all of them.
   const int ngroups = rows.ngroups();
+  auto step = [&](int gi, AttnGroup& cur, AttnGroup& ahead) {
+    rows.load(gi + DEPTH, ahead);
+    if (gi < ngroups) {
+      const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
+      consume(cur.k, cur.v, cur.valid, left >= ATT_GROUP ? ATT_R : (left + 31) / 32);
+    }
+  };
   AttnGroup& A = first;
-  for (int gi = 0; gi < ngroups; ++gi) {
+  if (DEPTH == 1) {
     AttnGroup B;
-    const bool more = gi + 1 < ngroups;
-    if (more) rows.load(gi + 1, B);
-    const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
-    consume(A.k, A.v, A.valid, left >= ATT_GROUP ? ATT_R : (left + 31) / 32);
-    if (more) A = B;
+    for (int gi = 0; gi < ngroups; gi += 2) {
+      step(gi, A, B);
+      step(gi + 1, B, A);
+    }
+  } else {
+    AttnGroup B, C;
+    rows.load(1, B);
+    for (int gi = 0; gi < ngroups; gi += 3) {
+      step(gi, A, C);
+      step(gi + 1, B, A);
+      step(gi + 2, C, B);
+    }
   }
   if (fresh) {   // the new row: row-lane 0 of one round
     const bool valid[1] = {rl == 0};
