@@ -43,7 +43,8 @@
 //     straight from HBM into LDS (buffer loads with the LDS bit), two 1 KiB
 //     chunks per poll round so the polls, which complete behind earlier
 //     loads, are not held up; attention items issue their cached K/V rows
-//     before they wait for q;
+//     before they wait for q; the workgroups with attention items get no O
+//     rows, so h1 does not wait for the last merge;
 //   * GEMVs are bf16 x bf16 -> fp32 with v_dot2_f32_bf16, reduced across the
 //     wave with DPP row operations and four lane reads (bs=1 is
 //     bandwidth-bound: no MFMA);
@@ -69,6 +70,7 @@ using namespace mk;
 constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
 constexpr int GU_LDS_STEP = 2;             // 1 KiB chunks of that copy issued per hand-over poll
+constexpr int O_RING = 4;                  // O rows per wave in the register ring
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -422,6 +424,18 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   if (pos_ok) {
     int R0, R1;
     share(H, G, w, R0, R1);
+    // O rows: the workgroups that run attention items (and merge the splits)
+    // get none, so h1 does not wait for the ones that finish attention last
+    int O0 = R0, O1 = R1;
+    {
+      int ns, rows;
+      attn_split(c.n_rows, ATT_MAX_SPLIT, 32, ns, rows);
+      const int A = NKV * ns;   // workgroups [0, A) run attention items
+      if (A <= G / 2) {
+        if (w < A) O0 = O1 = 0;
+        else share(H, G - A, w - A, O0, O1);
+      }
+    }
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
       const bool last = li == p.n_layers - 1;
@@ -436,9 +450,11 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       phase_attn(c, li, L);
 
       // ---- O projection + residual -> h1 ----
-      {
-        RowStream<2, 4> os;
-        const Span sp = wave_span(R0, R1);
+      if (O1 == O0) {
+        gpf.issue(GU_LDS_PAIRS * 8);
+      } else {
+        RowStream<O_RING, 4> os;
+        const Span sp = wave_span(O0, O1);
         os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
         trace_mark(c.s, 2 * xk(li, 3) - 1);
         stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, gidle);
@@ -449,12 +465,13 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         lds_x2048(L.v, xs);
         uint16_t* h1 = c.xb(li, X_H1);
         auto dotf = [&](const u32x4(&wv)[4]) { return dot2048(wv, xs); };
-        if (sp.n <= 2) {   // lanes 0-31: row 0, lanes 32-63: row 1
-          float pt[2];
+        if (sp.n <= O_RING) {   // one transposed reduction: row r in lanes 16r .. 16r+15
+          float pt[O_RING];
           os.dots(dotf, pt);
-          const float v = reduce_rows<2>(pt);
-          const int r = lane >> 5;
-          if ((lane & 31) == 0 && r < sp.n) st_dev(h1 + sp.lo + r, f2bf(bf2f(L.x[sp.lo + r]) + rbf(v)));
+          const float v = reduce_rows<O_RING>(pt);
+          const int r = lane / (64 / O_RING);
+          if ((lane & (64 / O_RING - 1)) == 0 && r < sp.n)
+            st_dev(h1 + sp.lo + r, f2bf(bf2f(L.x[sp.lo + r]) + rbf(v)));
         } else {
           float mine = 0.f;   // lane r: the wave's row r
           os.run(dotf, [&](int r, float part) {
