@@ -229,13 +229,14 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
   }
   wait_mem();
   __syncthreads();
-  // RMS per row: 8 threads (one lane octet) per row, chunks q8 + 8i (i < 32) of 8 elements
-  const int m = threadIdx.x >> 3, q8 = threadIdx.x & 7;
-  const bool rowv = m < 16 * MT;
-  float ss = 0.f;
-  if (rowv) {
-    for (int i = 0; i < 32; ++i) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][(q8 + 8 * i) * 8]);
+  // RMS per row: 16 threads (a 16-lane row of a wave) per token row, chunk q16 + 16i
+  // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped
+  const int q16 = threadIdx.x & 15;
+  for (int m = threadIdx.x >> 4; m < c.B; m += NT / 16) {
+    float ss = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * i) * 8]);
       const uint32_t e[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -244,14 +245,13 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
         ss = fmaf(b, b, ss);
       }
     }
-  }
-  ss = sum_lanes8(ss);
-  const float inv = rsqrtf(ss * (1.0f / H) + EPS);
-  if (rowv) {
-    for (int i = 0; i < 32; ++i) {
-      const int col = (q8 + 8 * i) * 8;
-      u32x4* px = reinterpret_cast<u32x4*>(&L.xn[m][col]);
-      const u32x4 x = *px;
+    ss = sum_lanes8(ss);
+    ss += dpp<DPP_ROR8>(ss);   // the 16 lanes of the row
+    const float inv = rsqrtf(ss * (1.0f / H) + EPS);
+#pragma unroll 2
+    for (int i = 0; i < 16; ++i) {
+      const int col = (q16 + 16 * i) * 8;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][col]);
       uint32_t e[4] = {x.x, x.y, x.z, x.w};
       if (col + 8 > r0 && col < r1) {
 #pragma unroll
@@ -263,14 +263,10 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
       const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        float a = rbf(bf_lo(e[k]) * inv), b = rbf(bf_hi(e[k]) * inv);
-        if (gamma) {
-          a = bf_lo(g[k]) * a;
-          b = bf_hi(g[k]) * b;
-        }
-        e[k] = pack_bf2(a, b);
+        const uint32_t n = cvt_bf2(bf_lo(e[k]) * inv, bf_hi(e[k]) * inv);
+        e[k] = gamma ? cvt_bf2(bf_lo(g[k]) * bf_lo(n), bf_hi(g[k]) * bf_hi(n)) : n;
       }
-      *px = u32x4{e[0], e[1], e[2], e[3]};
+      *reinterpret_cast<u32x4*>(&L.xn[m][col]) = u32x4{e[0], e[1], e[2], e[3]};
     }
   }
   __syncthreads();
