@@ -744,12 +744,49 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_PREFILL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   pos_ok = pos_ok && run_ok;
   if (pos_ok && t == 0) {
-    // attention items: about two per workgroup over all sequences' KV rows
-    long long total = 0;
-    for (int b = 0; b < c.B; ++b) total += (long long)NKV * (L.pos[b] + 1);
+    // Attention items (sequence, kv head, split of `tr` rows, a multiple of 32).
+    // The critical path is the busiest workgroup: about ceil(items / G) items
+    // of the longest split. Two plans: about two items per workgroup over all
+    // sequences' rows, or the shortest split that keeps every workgroup at one
+    // item (found by bisection). The second wins ragged batches, where the
+    // first's per-sequence rounding leaves some workgroups a third item; with
+    // equal lengths the first measured faster, so the second must be clearly
+    // shorter (by 10%) to be chosen.
+    auto plan = [&](long long rr, long long& n_items, long long& longest) {
+      n_items = 0;
+      longest = 0;
+      for (int b = 0; b < c.B; ++b) {
+        const long long n = L.pos[b] + 1;
+        long long ns = (n + rr - 1) / rr;
+        ns = ns < BATT_MAX_SPLIT ? ns : BATT_MAX_SPLIT;
+        const long long rows = ((n + ns - 1) / ns + 31) / 32 * 32;
+        n_items += NKV * ((n + rows - 1) / rows);
+        longest = rows > longest ? rows : longest;
+      }
+    };
+    long long total = 0, maxn = 0;
+    for (int b = 0; b < c.B; ++b) {
+      total += (long long)NKV * (L.pos[b] + 1);
+      maxn = L.pos[b] + 1 > maxn ? L.pos[b] + 1 : maxn;
+    }
     long long tr = (total + 2LL * c.G - 1) / (2LL * c.G);
     tr = (tr + 31) / 32 * 32;
     if (tr < ATT_MIN_ROWS) tr = ATT_MIN_ROWS;
+    long long ia, la, ib, lb;
+    plan(tr, ia, la);
+    long long lo = ATT_MIN_ROWS / 32, hi = (maxn + 31) / 32 > lo ? (maxn + 31) / 32 : lo;   // in units of 32 rows
+    plan(hi * 32, ib, lb);
+    if (ib <= c.G) {
+      while (lo < hi) {
+        const long long mid = (lo + hi) / 2;
+        plan(mid * 32, ib, lb);
+        if (ib <= c.G) hi = mid;
+        else lo = mid + 1;
+      }
+      plan(hi * 32, ib, lb);
+      const long long cost_a = (ia + c.G - 1) / c.G * la, cost_b = (ib + c.G - 1) / c.G * lb;
+      if (10 * cost_b < 9 * cost_a) tr = hi * 32;
+    }
     L.cum[0] = 0;
     for (int b = 0; b < c.B; ++b) {
       const int n = L.pos[b] + 1;

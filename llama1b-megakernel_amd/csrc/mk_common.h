@@ -584,7 +584,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
   // exactly the loads issued after it instead of falling back to waiting for all of them.
   const int ngroups = rows.ngroups();
   auto step = [&](int gi, AttnGroup& cur, AttnGroup& ahead) {
-    rows.load(gi + DEPTH, ahead);
+    rows.load(gi + DEPTH, ahead);   // past the last group: all rows invalid, nothing read
     if (gi < ngroups) {
       const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
       consume(cur.k, cur.v, cur.valid, left >= ATT_GROUP ? ATT_R : (left + 31) / 32);
