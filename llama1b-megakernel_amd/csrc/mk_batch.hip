@@ -112,6 +112,7 @@ struct BLds {
   __attribute__((aligned(16))) uint16_t res[16 * MT][RES_MAX];  // raw columns [R0, R1) of the staged input
   f32x4 red[NWAVE][MT][64];                                     // split-K partial tiles
   __attribute__((aligned(16))) uint16_t q[GQA * HD + 2 * HD];    // attention: 4 q heads | fresh k | fresh v
+  __attribute__((aligned(16))) uint16_t rope[16 * MT][2 * HD];   // each token's RoPE row: cos | sin
   AttnShared att;
   unsigned long long key[NWAVE][16 * MT];
   int pos[BATCH_MAX];
@@ -360,7 +361,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
         const int ps = L.pos[m];
         uint32_t outv;
         if (pr < Q_PAIRS + K_PAIRS) {
-          const u32x4 o = rope_pair(a, b, p.rope + (size_t)ps * (2 * HD), dd);
+          const u32x4 o = rope_pair(a, b, L.rope[m], dd);
           outv = hi ? o.y : o.x;
         } else {
           outv = f2bf(mine);
@@ -732,6 +733,13 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
   }
   __syncthreads();
+  // each token's RoPE row (read once; positions beyond the table are refused below)
+  for (int i = t; i < c.B * HD; i += NT) {
+    const int m = i / HD, ps = L.pos[m];
+    if (ps >= 0 && ps < p.rope_rows)
+      reinterpret_cast<uint32_t*>(L.rope[m])[i % HD] =
+          reinterpret_cast<const uint32_t*>(p.rope + (size_t)ps * (2 * HD))[i % HD];
+  }
   bool pos_ok = true, run_ok = true;
   for (int b = 0; b < c.B; ++b) {
     const int ps = L.pos[b];
