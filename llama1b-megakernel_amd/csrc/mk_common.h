@@ -361,7 +361,13 @@ __device__ __forceinline__ bool wait_expired(const Sync& s, unsigned long long t
 // OOB offsets read zero and count as ready) until the whole wave sees no
 // sentinel. A piece seen complete is not read again (its offset turns OOB),
 // so waiting consumers only re-read what is still missing. Called by full waves.
-// idle() runs before each round of polls (a caller issues background loads there).
+// idle() runs right after each round's poll loads are issued: a caller issues
+// background loads there. Loads complete in order, so a background load issued
+// before a poll would hold the poll's result back until it lands; issued after
+// it, and in a fixed number (so the wait can count past them), it does not.
+#ifndef MK_POLL_SLEEP
+#define MK_POLL_SLEEP 2
+#endif
 struct NoIdle {
   __device__ __forceinline__ void operator()() const {}
 };
@@ -373,10 +379,10 @@ __device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_
 #pragma unroll
   for (int i = 0; i < N; ++i) done[i] = false;
   for (int it = 1;; ++it) {
-    idle();
     u32x4 t[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) t[i] = ld_dev16(r, done[i] ? OOB : off[i]);
+    idle();
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -388,7 +394,7 @@ __device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_
     }
     if (__all(ok)) return;
     if (wait_expired(s, t0, it)) return;
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(MK_POLL_SLEEP);
   }
 }
 

@@ -69,7 +69,10 @@ using namespace mk;
 
 constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
-constexpr int GU_LDS_STEP = 2;             // 1 KiB chunks of that copy issued per hand-over poll
+#ifndef MK_GU_LDS_STEP
+#define MK_GU_LDS_STEP 3
+#endif
+constexpr int GU_LDS_STEP = MK_GU_LDS_STEP;   // 1 KiB chunks of that copy issued per hand-over poll
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
@@ -221,6 +224,24 @@ struct LdsPrefetch {
           off0 + (uint32_t)(next / kch) * stride + (uint32_t)(next % kch) * 1024u + (uint32_t)lane_id() * 16u, 0, 0,
           AUX_NT);
   }
+  // Exactly K copy instructions, a fixed count, so that a wait for loads
+  // issued just before them can count past them (vector loads complete in
+  // order): chunks beyond the copy go to `spare`, a 1 KiB LDS area nobody
+  // reads, from an out-of-range offset that reads no memory.
+  template <int K>
+  __device__ __forceinline__ void issue_fixed(uint8_t* spare) {
+    const int nx = __builtin_amdgcn_readfirstlane(next);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int ck = nx + k;
+      const bool real = ck < total;
+      uint8_t* d = real ? dst + ck * 1024 : spare;
+      const uint32_t o =
+          real ? off0 + (uint32_t)(ck / kch) * stride + (uint32_t)(ck % kch) * 1024u + (uint32_t)lane_id() * 16u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)d, 16, o, 0, 0, AUX_NT);
+    }
+    next = min(total, nx + K);
+  }
 };
 
 // GU pairs [0, GU_LDS_PAIRS) of this wave's share, HBM -> L.gu[wave] (pair j at j*8 KiB).
@@ -249,6 +270,7 @@ struct Lds {
   int bidx[NWAVE];
   int last;
   __attribute__((aligned(16))) uint8_t gu[NWAVE][GU_LDS_PAIRS * 8192];   // GU pairs copied ahead (per wave)
+  __attribute__((aligned(16))) uint8_t spare[1024];                       // target of padding copies
 };
 
 struct Ctx {
@@ -445,7 +467,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       // (vector loads complete in order), so the copy is spread out.
       GuPrefetch gpf;
       gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, G, w, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
-      auto gidle = [&]() { gpf.issue(GU_LDS_STEP); };
+      auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP>(L.spare); };
       phase_qkv(c, li, L, gidle);
       phase_attn(c, li, L);
 
