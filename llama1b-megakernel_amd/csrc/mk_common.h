@@ -314,6 +314,15 @@ __device__ __forceinline__ uint32_t ld_dev4(rsrc_t r, uint32_t off) {
 // Completion of this wave's outstanding memory operations (stores included).
 __device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier for data exchanged through LDS by ds_write / ds_read.
+// __syncthreads() (and an LDS-only fence, once a wave has HBM -> LDS copies in
+// flight) also waits for every outstanding global load and store of the wave
+// (s_waitcnt vmcnt(0)), which holds the barrier back until weight streams and
+// background copies issued before it have landed; this one leaves them in
+// flight. A wave reads an LDS area written by its own HBM -> LDS copies only
+// after wait_mem().
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
@@ -628,7 +637,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     reduce_stride8<GQA, true>(mv);   // lane: head 2*b5 + b4
     if ((lane & 15) == 0) sh.mx[wave][lane >> 4] = mv[0];
   }
-  __syncthreads();
+  lds_sync();
   {
     float lv[GQA], av[GQA * 8];
 #pragma unroll
@@ -644,7 +653,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     reduce_stride8<GQA * 8, false>(av);   // lane: values 4*(lane >> 3) .. +3 of head-major [4][8]
     *reinterpret_cast<float4*>(&sh.pv[wave][ch][(lane >> 3) * 4]) = make_float4(av[0], av[1], av[2], av[3]);
   }
-  __syncthreads();
+  lds_sync();
   {
     const int g = t >> 6, d = t & 63;
     float o = 0.f;
@@ -656,7 +665,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
       st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
     }
   }
-  __syncthreads();   // LDS reuse by a following item
+  lds_sync();   // LDS reuse by a following item
 }
 
 // Split of [0, n_rows) into nsplit items of `rows` rows (a multiple of 32):

@@ -321,7 +321,7 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li == 0) stage_vec<1>(c.s, c.x_in, false, L.x);
   else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x, idle);
-  __syncthreads();
+  lds_sync();
   trace_mark(c.s, 2 * xk(li, 1));
   u32x4 xs[4];
   lds_x2048(L.x, xs);
@@ -339,7 +339,7 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
       if (lane_id() == 0) L.val[wave + NWAVE * r] = v;
     });
   }
-  __syncthreads();
+  lds_sync();
   const uint16_t* rrow = L.rope;
   uint16_t* xq = c.xb(li, X_QKV);
   for (int lp = threadIdx.x; lp < P1 - P0; lp += NT) {
@@ -394,7 +394,7 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
       poll_bf16<1>(c.s, r, off, v);
       if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v[0];
     }
-    __syncthreads();
+    lds_sync();
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2));
     attn_item(ar, g0, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
     if (sp == 0)
@@ -441,7 +441,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   if (pos_ok && threadIdx.x < HD)   // the step's RoPE row, read once
     reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] =
         reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
-  __syncthreads();
+  lds_sync();
 
   if (pos_ok) {
     int R0, R1;
@@ -481,7 +481,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         trace_mark(c.s, 2 * xk(li, 3) - 1);
         stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, gidle);
         gpf.issue(GU_LDS_PAIRS * 8);   // whatever the waits left
-        __syncthreads();
+        lds_sync();
         trace_mark(c.s, 2 * xk(li, 3));
         u32x4 xs[4];
         lds_x2048(L.v, xs);
@@ -515,7 +515,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  (uint32_t)(sp.lo + n_lds) * (2 * H * 2), 2 * H * 2, sp.n - n_lds);
         trace_mark(c.s, 2 * xk(li, 4) - 1);
         stage_vec<1>(c.s, c.xb(li, X_H1), true, L.h1);
-        __syncthreads();
+        lds_sync();
         trace_mark(c.s, 2 * xk(li, 4));
         u32x4 xs[4];
         lds_x2048(L.h1, xs);
@@ -582,7 +582,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
                  sp.n);
         trace_mark(c.s, 2 * xk(li, 5) - 1);
         stage_vec<4>(c.s, c.xb(li, X_ACT), true, L.v);
-        __syncthreads();
+        lds_sync();
         trace_mark(c.s, 2 * xk(li, 5));
         uint16_t* h2 = c.xb(li, X_H2);
         u32x4 xs[16];
@@ -629,7 +629,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       ls.start(make_rsrc(p.embed, EMBED_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
       trace_mark(c.s, 2 * xk(p.n_layers, 1) - 1);
       stage_vec<1>(c.s, c.xb(p.n_layers - 1, X_H2), true, L.x);
-      __syncthreads();
+      lds_sync();
       trace_mark(c.s, 2 * xk(p.n_layers, 1));
       u32x4 xs[4];
       lds_x2048(L.x, xs);
