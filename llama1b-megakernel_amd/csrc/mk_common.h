@@ -374,9 +374,6 @@ __device__ __forceinline__ bool wait_expired(const Sync& s, unsigned long long t
 // background loads there. Loads complete in order, so a background load issued
 // before a poll would hold the poll's result back until it lands; issued after
 // it, and in a fixed number (so the wait can count past them), it does not.
-#ifndef MK_POLL_SLEEP
-#define MK_POLL_SLEEP 2
-#endif
 struct NoIdle {
   __device__ __forceinline__ void operator()() const {}
 };
@@ -403,7 +400,7 @@ __device__ __forceinline__ void poll_bf16(const Sync& s, rsrc_t r, const uint32_
     }
     if (__all(ok)) return;
     if (wait_expired(s, t0, it)) return;
-    __builtin_amdgcn_s_sleep(MK_POLL_SLEEP);
+    __builtin_amdgcn_s_sleep(2);
   }
 }
 

@@ -69,10 +69,9 @@ using namespace mk;
 
 constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
-#ifndef MK_GU_LDS_STEP
-#define MK_GU_LDS_STEP 3
-#endif
-constexpr int GU_LDS_STEP = MK_GU_LDS_STEP;   // 1 KiB chunks of that copy issued per hand-over poll
+// 1 KiB chunks of that copy issued per poll round of the layer-input wait and
+// of the attention-output wait
+constexpr int GU_LDS_STEP_QKV = 2, GU_LDS_STEP_O = 4;
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
@@ -467,7 +466,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       // (vector loads complete in order), so the copy is spread out.
       GuPrefetch gpf;
       gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, G, w, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
-      auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP>(L.spare); };
+      auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
+      auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
       phase_qkv(c, li, L, gidle);
       phase_attn(c, li, L);
 
@@ -479,7 +479,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         const Span sp = wave_span(O0, O1);
         os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
         trace_mark(c.s, 2 * xk(li, 3) - 1);
-        stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, gidle);
+        stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, oidle);
         gpf.issue(GU_LDS_PAIRS * 8);   // whatever the waits left
         lds_sync();
         trace_mark(c.s, 2 * xk(li, 3));
