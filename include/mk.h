@@ -154,11 +154,15 @@ typedef struct mk_step_args {
      * Hand-over k = 5*i + j is phase j of run-layer i (1 QKV input, 2
      * attention inputs, recorded by workgroups with attention work only, 3
      * attention output, 4 h1, 5 gate/up output); k = 5*n_layers + 1 is the
-     * lm_head input. */
+     * lm_head input. Slot MK_TRACE_DONE0 + 5*i + j (below MK_TRACE_SLOTS-8)
+     * is recorded when phase j (0 QKV, 1 attention, 2 O, 3 gate/up, 4 down)
+     * of run-layer i has issued its result stores; slots MK_TRACE_SLOTS-8 ..
+     * MK_TRACE_SLOTS-2 hold kernel-specific diagnostic values. */
     void *trace;
 } mk_step_args;
 
 #define MK_TRACE_SLOTS 256
+#define MK_TRACE_DONE0 166
 
 /*
  * On-device sampling of the next token from fp32 logits (after a decode step

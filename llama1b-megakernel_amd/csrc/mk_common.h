@@ -312,7 +312,9 @@ __device__ __forceinline__ uint32_t ld_dev4(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX_SC1);
 }
 // Completion of this wave's outstanding memory operations (stores included).
-__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// (The builtin, not inline assembly: the compiler's own wait insertion then
+// knows that nothing issued before it is still outstanding.)
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0x0f70); }   // vmcnt(0)
 
 // Workgroup barrier for data exchanged through LDS by ds_write / ds_read.
 // __syncthreads() (and an LDS-only fence, once a wave has HBM -> LDS copies in
@@ -350,6 +352,15 @@ struct Sync {
 
 __device__ __forceinline__ void trace_mark(const Sync& s, int slot) {
   if (s.trace && threadIdx.x == 0 && slot < MK_TRACE_SLOTS) s.trace[slot] = wall_clock64();
+}
+// Slot MK_TRACE_DONE0 + 5*li + j: phase j (0 QKV, 1 ATTN, 2 O, 3 GU, 4 DOWN) of
+// run-layer li has issued its result stores.
+__device__ __forceinline__ void trace_done(const Sync& s, int li, int j) {
+  if (MK_TRACE_DONE0 + 5 * li + j < MK_TRACE_SLOTS - 8) trace_mark(s, MK_TRACE_DONE0 + 5 * li + j);
+}
+// A diagnostic value (not a time) in one of the slots MK_TRACE_SLOTS-8 .. -2.
+__device__ __forceinline__ void trace_value(const Sync& s, int k, unsigned long long v) {
+  if (s.trace && threadIdx.x == 0 && k >= 0 && k < 7) s.trace[MK_TRACE_SLOTS - 8 + k] = v;
 }
 
 // True when a wait must give up: its time limit passed (the error bit is set
@@ -625,6 +636,10 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
                                   : u32x4{0u, 0u, 0u, 0u}};
     consume(kk, vv, valid, 1);
   }
+  // The loads issued ahead past the last group read nothing (out of range);
+  // drain them now, while nothing else is in flight, so that no later code
+  // reusing their registers waits for the stores and copies issued after them.
+  wait_mem();
   // merge the 32 row-lanes of the item (lane bits 3-5 within a wave, then the
   // 4 waves through LDS): max, rescale, sum. The lanes of one row agree.
   {

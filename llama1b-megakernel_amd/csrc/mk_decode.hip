@@ -73,6 +73,16 @@ constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM 
 // of the attention-output wait
 constexpr int GU_LDS_STEP_QKV = 2, GU_LDS_STEP_O = 4;
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
+// Gate/up pairs per wave (after the LDS ones) loaded into registers before the
+// attention-output wait on workgroups with O rows, so that the h1 wait queues
+// behind fewer weight loads; the other GU_RING pairs of the wave's first eight
+// are issued after the O projection.
+#ifndef MK_GU_EARLY
+#define MK_GU_EARLY 1
+#endif
+constexpr int GU_EARLY = MK_GU_EARLY;
+constexpr int GU_RING = 4 - GU_EARLY;
+static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -165,6 +175,10 @@ struct RowStream {
     for (int j = 0; j < RING; ++j) part[j] = dotf(buf[j]);
   }
   // dotf(buf) -> partial (per lane); emit(r, partial) for each valid row r.
+  // The last RING refills are past the rows (out of range, nothing read); they
+  // are drained here, so that no later code that reuses the ring's registers
+  // has to wait for every memory operation issued meanwhile (result stores
+  // and background copies included).
   template <class DotF, class EmitF>
   __device__ __forceinline__ void run(DotF&& dotf, EmitF&& emit) {
     for (int base = 0; base < n; base += RING) {
@@ -176,6 +190,7 @@ struct RowStream {
         if (r < n) emit(r, part);
       }
     }
+    wait_mem();
   }
 };
 
@@ -245,12 +260,25 @@ struct LdsPrefetch {
 
 // GU pairs [0, GU_LDS_PAIRS) of this wave's share, HBM -> L.gu[wave] (pair j at j*8 KiB).
 struct GuPrefetch : LdsPrefetch {
-  __device__ __forceinline__ void start(const uint16_t* w_gu_layer, int G, int w, uint8_t* region) {
-    int U0, U1;
-    share(INTER, G, w, U0, U1);
-    const Span gp = wave_span(U0, U1);
+  __device__ __forceinline__ void start(const uint16_t* w_gu_layer, Span gp, uint8_t* region) {
     init(make_rsrc(w_gu_layer, GU_LAYER_BYTES), (uint32_t)gp.lo * (2 * H * 2), 2 * H * 2, 8,
          min(gp.n, GU_LDS_PAIRS), region);
+  }
+};
+
+// Gate/up pairs [n_lds, n_lds + GU_EARLY) of the wave's share in registers
+// (pairs past the share read zero from out-of-range offsets).
+struct GuEarly {
+  u32x4 buf[GU_EARLY > 0 ? GU_EARLY : 1][8];
+  __device__ __forceinline__ void issue(const uint16_t* w_gu_layer, Span sp, int n_lds) {
+    const rsrc_t r = make_rsrc(w_gu_layer, GU_LAYER_BYTES);
+#pragma unroll
+    for (int j = 0; j < GU_EARLY; ++j) {
+      const int row = n_lds + j;
+      const uint32_t o = (row < sp.n ? (uint32_t)(sp.lo + row) * (2 * H * 2) : OOB) + (uint32_t)lane_id() * 16u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) buf[j][i] = ld_stream(r, o + (uint32_t)i * 1024u);
+    }
   }
 };
 
@@ -280,6 +308,15 @@ struct Ctx {
   int n_rows;            // KV rows attended: pos + 1
   const uint16_t* x_in;  // input of the first layer (embedding row or hidden_in): final data
   uint8_t* set;          // this launch's exchange buffers
+  // Work split, the same for every layer (computed once per launch: the
+  // divisions by the grid size are not cheap on the GPU)
+  int P0, P1;            // QKV RoPE pairs of the workgroup
+  int qkv_n;             // QKV rows of this wave: 2*P0 + wave + 4*j, j < qkv_n
+  int nsplit, att_rows;  // attention: KV splits per kv head, rows per split
+  Span o_rows;           // this wave's O rows (empty on workgroups with attention items)
+  bool has_o;            // the workgroup has O rows
+  Span gu_pairs;         // this wave's gate/up pairs
+  Span d_rows;           // this wave's down-projection rows
 
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
     return reinterpret_cast<uint16_t*>(set + (size_t)li * X_LAYER + off);
@@ -295,11 +332,9 @@ __device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
 // The wave's QKV weight rows of run-layer li: rows 2*P0 + wave + 4*j, j < n.
 __device__ __forceinline__ void qkv_rows(const Ctx& c, int li, rsrc_t& r, uint32_t& off0, int& n) {
   const KParams& p = *c.p;
-  int P0, P1;
-  share(QKV_PAIRS, c.G, c.w, P0, P1);
   r = make_rsrc(p.w_qkv + (size_t)(p.first_layer + li) * QKV_ROWS * H, QKV_LAYER_BYTES);
-  off0 = (uint32_t)(2 * P0 + wave_id()) * (H * 2);
-  n = wave_count(0, 2 * (P1 - P0));
+  off0 = (uint32_t)(2 * c.P0 + wave_id()) * (H * 2);
+  n = c.qkv_n;
 }
 
 // QKV phase of run-layer li: RMSNorm, GEMV, RoPE; q and the fresh K/V row to
@@ -309,8 +344,7 @@ template <class Idle>
 __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   const KParams& p = *c.p;
   const int wave = wave_id();
-  int P0, P1;
-  share(QKV_PAIRS, c.G, c.w, P0, P1);
+  const int P0 = c.P0, P1 = c.P1;
   rsrc_t wr;
   uint32_t woff;
   int wn;
@@ -341,6 +375,8 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   lds_sync();
   const uint16_t* rrow = L.rope;
   uint16_t* xq = c.xb(li, X_QKV);
+  uint16_t* const kcl = p.kc[li];
+  uint16_t* const vcl = p.vc[li];
   for (int lp = threadIdx.x; lp < P1 - P0; lp += NT) {
     const int pr = P0 + lp, d = pr & 31;
     const float a = rbf(L.val[2 * lp]), b = rbf(L.val[2 * lp + 1]);
@@ -357,17 +393,17 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
       st_dev(dst, o.x);
       st_dev(dst + 32, o.y);
       // the cache row is read only by later launches: a plain store
-      uint16_t* crow = (is_k ? p.kc[li] : p.vc[li]) + ((size_t)kh * p.s_max + c.pos) * HD + d;
+      uint16_t* crow = (is_k ? kcl : vcl) + ((size_t)kh * p.s_max + c.pos) * HD + d;
       crow[0] = (uint16_t)o.x;
       crow[32] = (uint16_t)o.y;
     }
   }
+  trace_done(c.s, li, 0);
 }
 
 // ATTN phase: the workgroup's attention items (kv head, KV split).
 __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
-  int nsplit, rows;
-  attn_split(c.n_rows, ATT_MAX_SPLIT, 32, nsplit, rows);
+  const int nsplit = c.nsplit, rows = c.att_rows;
   const int nitems = NKV * nsplit;
   const int lane = lane_id();
   for (int it = c.w; it < nitems; it += c.G) {
@@ -399,6 +435,7 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     if (sp == 0)
       attn_merge_head<true, ATT_MAX_SPLIT>(c.s, c.part(li) + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS, nsplit,
                                            c.xb(li, X_ATT) + h * GQA * HD);
+    trace_done(c.s, li, 1);
   }
 }
 
@@ -443,19 +480,26 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   lds_sync();
 
   if (pos_ok) {
-    int R0, R1;
-    share(H, G, w, R0, R1);
-    // O rows: the workgroups that run attention items (and merge the splits)
-    // get none, so h1 does not wait for the ones that finish attention last
-    int O0 = R0, O1 = R1;
     {
-      int ns, rows;
-      attn_split(c.n_rows, ATT_MAX_SPLIT, 32, ns, rows);
-      const int A = NKV * ns;   // workgroups [0, A) run attention items
+      share(QKV_PAIRS, G, w, c.P0, c.P1);
+      c.qkv_n = wave_count(0, 2 * (c.P1 - c.P0));
+      attn_split(c.n_rows, ATT_MAX_SPLIT, 32, c.nsplit, c.att_rows);
+      int R0, R1;
+      share(H, G, w, R0, R1);
+      c.d_rows = wave_span(R0, R1);
+      // O rows: the workgroups that run attention items (and merge the splits)
+      // get none, so h1 does not wait for the ones that finish attention last
+      int O0 = R0, O1 = R1;
+      const int A = NKV * c.nsplit;   // workgroups [0, A) run attention items
       if (A <= G / 2) {
         if (w < A) O0 = O1 = 0;
         else share(H, G - A, w - A, O0, O1);
       }
+      c.o_rows = wave_span(O0, O1);
+      c.has_o = O1 > O0;
+      int U0, U1;
+      share(INTER, G, w, U0, U1);
+      c.gu_pairs = wave_span(U0, U1);
     }
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
@@ -465,21 +509,27 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       // a few chunks per poll round: the hand-over polls queue behind them
       // (vector loads complete in order), so the copy is spread out.
       GuPrefetch gpf;
-      gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, G, w, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
+      gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, c.gu_pairs, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
       phase_qkv(c, li, L, gidle);
+      if (li == 8) trace_value(c.s, 1, (unsigned long long)gpf.next);
       phase_attn(c, li, L);
 
       // ---- O projection + residual -> h1 ----
-      if (O1 == O0) {
+      const uint16_t* w_gu_l = p.w_gu + (size_t)l * 2 * INTER * H;
+      GuEarly ge;
+      if (!c.has_o) {
         gpf.issue(GU_LDS_PAIRS * 8);
+        ge.issue(w_gu_l, c.gu_pairs, gpf.total / 8);
       } else {
         RowStream<O_RING, 4> os;
-        const Span sp = wave_span(O0, O1);
+        const Span sp = c.o_rows;
         os.start(make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
+        ge.issue(w_gu_l, c.gu_pairs, gpf.total / 8);
         trace_mark(c.s, 2 * xk(li, 3) - 1);
         stage_vec<1>(c.s, c.xb(li, X_ATT), true, L.v, oidle);
+        if (li == 8) trace_value(c.s, 0, (unsigned long long)gpf.next);
         gpf.issue(GU_LDS_PAIRS * 8);   // whatever the waits left
         lds_sync();
         trace_mark(c.s, 2 * xk(li, 3));
@@ -502,17 +552,17 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           });
           if (lane < sp.n) st_dev(h1 + sp.lo + lane, f2bf(bf2f(L.x[sp.lo + lane]) + rbf(mine)));
         }
+        trace_done(c.s, li, 2);
       }
 
       // ---- gate/up + SwiGLU -> act ----
       {
-        int U0, U1;
-        share(INTER, G, w, U0, U1);
-        RowStream<4, 8> gs;
-        const Span sp = wave_span(U0, U1);
-        const int n_lds = gpf.total / 8;   // pairs [0, n_lds) are in LDS
-        gs.start(make_rsrc(p.w_gu + (size_t)l * 2 * INTER * H, GU_LAYER_BYTES),
-                 (uint32_t)(sp.lo + n_lds) * (2 * H * 2), 2 * H * 2, sp.n - n_lds);
+        RowStream<GU_RING, 8> gs;
+        const Span sp = c.gu_pairs;
+        const int n_lds = gpf.total / 8;   // pairs [0, n_lds) are in LDS, the next GU_EARLY in ge
+        const int n_reg = min(GU_EARLY, sp.n - n_lds);
+        gs.start(make_rsrc(w_gu_l, GU_LAYER_BYTES), (uint32_t)(sp.lo + n_lds + n_reg) * (2 * H * 2), 2 * H * 2,
+                 sp.n - n_lds - n_reg);
         trace_mark(c.s, 2 * xk(li, 4) - 1);
         stage_vec<1>(c.s, c.xb(li, X_H1), true, L.h1);
         lds_sync();
@@ -551,12 +601,18 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
             pt[j] = d.g;
             pt[8 + j] = d.u;
           }
-          GU2 rp[4];
+#pragma unroll
+          for (int j = 0; j < GU_EARLY; ++j) {
+            const GU2 d = gu_dot(ge.buf[j]);
+            pt[GU_LDS_PAIRS + j] = d.g;
+            pt[8 + GU_LDS_PAIRS + j] = d.u;
+          }
+          GU2 rp[GU_RING];
           gs.dots(gu_dot, rp);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            pt[GU_LDS_PAIRS + j] = rp[j].g;
-            pt[8 + GU_LDS_PAIRS + j] = rp[j].u;
+          for (int j = 0; j < GU_RING; ++j) {
+            pt[GU_LDS_PAIRS + GU_EARLY + j] = rp[j].g;
+            pt[8 + GU_LDS_PAIRS + GU_EARLY + j] = rp[j].u;
           }
           const float v = reduce_rows<16>(pt);   // lane 4k..4k+3: row k
           const Pair gu = xor32_pair(v);         // lanes 0-31: g (own) and u (lane + 32)
@@ -569,15 +625,19 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
             for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
             gu_emit(j, gu_dot(wv));
           }
-          gs.run(gu_dot, [&](int r, GU2 part) { gu_emit(n_lds + r, part); });
+#pragma unroll
+          for (int j = 0; j < GU_EARLY; ++j)
+            if (j < n_reg) gu_emit(n_lds + j, gu_dot(ge.buf[j]));
+          gs.run(gu_dot, [&](int r, GU2 part) { gu_emit(n_lds + n_reg + r, part); });
           if (lane < sp.n) st_dev(act + sp.lo + lane, f2bf(mine));
         }
+        trace_done(c.s, li, 3);
       }
 
       // ---- down projection + residual -> h2 ----
       {
         RowStream<2, 16> ds;
-        const Span sp = wave_span(R0, R1);
+        const Span sp = c.d_rows;
         ds.start(make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES), (uint32_t)sp.lo * (INTER * 2), INTER * 2,
                  sp.n);
         trace_mark(c.s, 2 * xk(li, 5) - 1);
@@ -617,6 +677,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           });
           if (lane < sp.n) out(lane, mine);
         }
+        trace_done(c.s, li, 4);
       }
     }
 
