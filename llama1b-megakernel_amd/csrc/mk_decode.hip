@@ -71,18 +71,43 @@ constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (atte
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
 // 1 KiB chunks of that copy issued per poll round of the layer-input wait and
 // of the attention-output wait
-constexpr int GU_LDS_STEP_QKV = 2, GU_LDS_STEP_O = 4;
+#ifndef MK_GU_STEP_QKV
+#define MK_GU_STEP_QKV 6
+#endif
+#ifndef MK_GU_STEP_O
+#define MK_GU_STEP_O 4
+#endif
+constexpr int GU_LDS_STEP_QKV = MK_GU_STEP_QKV, GU_LDS_STEP_O = MK_GU_STEP_O;
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
 // Gate/up pairs per wave (after the LDS ones) loaded into registers before the
 // attention-output wait on workgroups with O rows, so that the h1 wait queues
 // behind fewer weight loads; the other GU_RING pairs of the wave's first eight
 // are issued after the O projection.
 #ifndef MK_GU_EARLY
-#define MK_GU_EARLY 1
+#define MK_GU_EARLY 2
 #endif
 constexpr int GU_EARLY = MK_GU_EARLY;
 constexpr int GU_RING = 4 - GU_EARLY;
 static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
+// 1 KiB chunks of the wave's first down-projection row loaded before the
+// gate/up dot products (they land while those run, so the act store that
+// queues behind them is not delayed, and HBM is not idle meanwhile).
+#ifndef MK_D_EARLY
+#define MK_D_EARLY 8
+#endif
+constexpr int D_EARLY = MK_D_EARLY;
+static_assert(D_EARLY >= 0 && D_EARLY <= 16, "down-projection early chunks");
+// The wave's first QKV row of the next layer loaded before the down-projection
+// dot products (1), and gate/up copy chunks issued when the layer input has
+// arrived, before the QKV dot products (MK_QKV_COPY), for the same reason.
+#ifndef MK_Q_EARLY
+#define MK_Q_EARLY 0
+#endif
+#ifndef MK_QKV_COPY
+#define MK_QKV_COPY 0
+#endif
+constexpr bool Q_EARLY = MK_Q_EARLY != 0;
+constexpr int QKV_COPY = MK_QKV_COPY;
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -154,18 +179,19 @@ struct RowStream {
   __device__ __forceinline__ uint32_t row_off(int r) const {
     return r < n ? off0 + (uint32_t)r * stride : OOB;
   }
-  __device__ __forceinline__ void issue(int slot_row, u32x4 (&dst)[KCH]) const {
+  // Chunks i < skip read nothing (zero): the caller has loaded them already.
+  __device__ __forceinline__ void issue(int slot_row, u32x4 (&dst)[KCH], int skip = 0) const {
     const uint32_t o = row_off(slot_row) + (uint32_t)lane_id() * 16u;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) dst[i] = ld_stream(rs, o + (uint32_t)i * 1024u);
+    for (int i = 0; i < KCH; ++i) dst[i] = ld_stream(rs, i < skip ? OOB : o + (uint32_t)i * 1024u);
   }
-  __device__ __forceinline__ void start(rsrc_t r, uint32_t o0, uint32_t st, int count) {
+  __device__ __forceinline__ void start(rsrc_t r, uint32_t o0, uint32_t st, int count, int skip0 = 0) {
     rs = r;
     off0 = o0;
     stride = st;
     n = count;
 #pragma unroll
-    for (int j = 0; j < RING; ++j) issue(j, buf[j]);
+    for (int j = 0; j < RING; ++j) issue(j, buf[j], j == 0 ? skip0 : 0);
   }
   // When n <= RING: the per-lane partials of all RING slots (rows >= n read
   // zero, so their partials are 0), with no refill loads.
@@ -340,8 +366,12 @@ __device__ __forceinline__ void qkv_rows(const Ctx& c, int li, rsrc_t& r, uint32
 // QKV phase of run-layer li: RMSNorm, GEMV, RoPE; q and the fresh K/V row to
 // the exchange buffer, the K/V row also into the caches. idle() runs between
 // the polls for the layer input.
-template <class Idle>
-__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
+// qpre: the wave's first QKV row of this layer, already loaded when use_pre
+// (the ring then reads that row's chunks as zero). post() runs once the layer
+// input has arrived, before the dot products.
+template <class Idle, class Post>
+__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, const u32x4 (&qpre)[4], bool use_pre,
+                                          Post&& post) {
   const KParams& p = *c.p;
   const int wave = wave_id();
   const int P0 = c.P0, P1 = c.P1;
@@ -350,12 +380,13 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   int wn;
   qkv_rows(c, li, wr, woff, wn);
   RowStream<4, 4> rs;
-  rs.start(wr, woff, NWAVE * H * 2, wn);
+  rs.start(wr, woff, NWAVE * H * 2, wn, use_pre ? 4 : 0);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li == 0) stage_vec<1>(c.s, c.x_in, false, L.x);
   else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x, idle);
   lds_sync();
   trace_mark(c.s, 2 * xk(li, 1));
+  post();
   u32x4 xs[4];
   lds_x2048(L.x, xs);
   rmsnorm2048(xs, nullptr);
@@ -363,6 +394,7 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   if (wn <= 4) {   // all rows in the ring: one transposed reduction
     float pt[4];
     rs.dots(dotf, pt);
+    if (use_pre) pt[0] += dot2048(qpre, xs);
     const float v = reduce_rows<4>(pt);
     const int r = lane_id() >> 4;
     if ((lane_id() & 15) == 0 && r < wn) L.val[wave + NWAVE * r] = v;
@@ -501,6 +533,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       share(INTER, G, w, U0, U1);
       c.gu_pairs = wave_span(U0, U1);
     }
+    u32x4 qpre[4];   // the next layer's first QKV row of the wave (Q_EARLY)
+    bool qpre_ok = false;
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
       const bool last = li == p.n_layers - 1;
@@ -512,7 +546,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, c.gu_pairs, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
-      phase_qkv(c, li, L, gidle);
+      phase_qkv(c, li, L, gidle, qpre, qpre_ok, [&]() { gpf.issue_fixed<QKV_COPY>(L.spare); });
+      qpre_ok = false;
       if (li == 8) trace_value(c.s, 1, (unsigned long long)gpf.next);
       phase_attn(c, li, L);
 
@@ -556,6 +591,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       }
 
       // ---- gate/up + SwiGLU -> act ----
+      const rsrc_t rd = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
+      const bool d_fast = c.d_rows.n <= 2;
+      u32x4 dpre[D_EARLY > 0 ? D_EARLY : 1];
       {
         RowStream<GU_RING, 8> gs;
         const Span sp = c.gu_pairs;
@@ -588,15 +626,25 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           if (lane == r) mine = gv / (1.0f + __expf(-gv)) * uv;
         };
         wait_mem();   // this wave's LDS copy (and the ring) have landed
+        // the first D_EARLY chunks of the wave's first down row (fast down path only)
+        {
+          const uint32_t o =
+              (d_fast && c.d_rows.n > 0 ? (uint32_t)c.d_rows.lo * (INTER * 2) : OOB) + (uint32_t)lane * 16u;
+#pragma unroll
+          for (int i = 0; i < D_EARLY; ++i) dpre[i] = ld_stream(rd, o + (uint32_t)i * 1024u);
+        }
         const uint8_t* src = L.gu[wave];
+        auto lds_pair = [&](int j, u32x4(&wv)[8]) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
+        };
         if (n_lds == GU_LDS_PAIRS && sp.n - n_lds <= 4) {
           // 8 pairs: 16 rows (g of pairs 0-7, then u) in one transposed reduction
           float pt[16];
 #pragma unroll
           for (int j = 0; j < GU_LDS_PAIRS; ++j) {
             u32x4 wv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
+            lds_pair(j, wv);
             const GU2 d = gu_dot(wv);
             pt[j] = d.g;
             pt[8 + j] = d.u;
@@ -614,6 +662,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
             pt[GU_LDS_PAIRS + GU_EARLY + j] = rp[j].g;
             pt[8 + GU_LDS_PAIRS + GU_EARLY + j] = rp[j].u;
           }
+
           const float v = reduce_rows<16>(pt);   // lane 4k..4k+3: row k
           const Pair gu = xor32_pair(v);         // lanes 0-31: g (own) and u (lane + 32)
           const int r = lane >> 2;
@@ -621,8 +670,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         } else {
           for (int j = 0; j < n_lds; ++j) {
             u32x4 wv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(src + (j * 8 + i) * 1024 + lane * 16);
+            lds_pair(j, wv);
             gu_emit(j, gu_dot(wv));
           }
 #pragma unroll
@@ -638,12 +686,21 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       {
         RowStream<2, 16> ds;
         const Span sp = c.d_rows;
-        ds.start(make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES), (uint32_t)sp.lo * (INTER * 2), INTER * 2,
-                 sp.n);
+        ds.start(rd, (uint32_t)sp.lo * (INTER * 2), INTER * 2, sp.n, d_fast ? D_EARLY : 0);
         trace_mark(c.s, 2 * xk(li, 5) - 1);
         stage_vec<4>(c.s, c.xb(li, X_ACT), true, L.v);
         lds_sync();
         trace_mark(c.s, 2 * xk(li, 5));
+        if (Q_EARLY && li + 1 < p.n_layers && c.qkv_n <= 4) {
+          rsrc_t qr;
+          uint32_t qo;
+          int qn;
+          qkv_rows(c, li + 1, qr, qo, qn);
+          const uint32_t o = (qn > 0 ? qo : OOB) + (uint32_t)lane * 16u;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qpre[i] = ld_stream(qr, o + (uint32_t)i * 1024u);
+          qpre_ok = true;
+        }
         uint16_t* h2 = c.xb(li, X_H2);
         u32x4 xs[16];
 #pragma unroll
@@ -666,6 +723,12 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         if (sp.n <= 2) {   // lanes 0-31: row 0, lanes 32-63: row 1
           float pt[2];
           ds.dots(dotf, pt);
+          {   // row 0's first D_EARLY chunks (read as zero by the ring)
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < D_EARLY; ++i) a = dot8(dpre[i], xs[i], a);
+            pt[0] += a;
+          }
           const float v = reduce_rows<2>(pt);
           const int r = lane >> 5;
           if ((lane & 31) == 0 && r < sp.n) out(r, v);
