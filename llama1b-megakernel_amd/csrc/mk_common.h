@@ -329,9 +329,15 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 // Contiguous share [lo, hi) of `total` items for part `i` of `n`.
+// (32-bit division when the products fit: much shorter than the 64-bit one.)
 __device__ __forceinline__ void share(int total, int n, int i, int& lo, int& hi) {
-  lo = (int)(((long long)total * i) / n);
-  hi = (int)(((long long)total * (i + 1)) / n);
+  if ((unsigned long long)(unsigned)total * (unsigned)n <= 0xffffffffull) {
+    lo = (int)(((uint32_t)total * (uint32_t)i) / (uint32_t)n);
+    hi = (int)(((uint32_t)total * (uint32_t)(i + 1)) / (uint32_t)n);
+  } else {
+    lo = (int)(((long long)total * i) / n);
+    hi = (int)(((long long)total * (i + 1)) / n);
+  }
 }
 
 // Sentinel tests. bf16 exchange data: any 16-bit lane equal to 0xffff.

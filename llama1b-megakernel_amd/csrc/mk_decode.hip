@@ -38,13 +38,19 @@
 //   * before polling for its input each wave has already issued the first
 //     ring of the phase's weight loads (they do not depend on the
 //     activations), so the hand-over latency overlaps HBM traffic;
-//   * the attention and O hand-overs leave HBM mostly idle, so during them
-//     each wave copies the first 4 gate/up pairs of its GU share (32 KiB)
-//     straight from HBM into LDS (buffer loads with the LDS bit), two 1 KiB
-//     chunks per poll round so the polls, which complete behind earlier
-//     loads, are not held up; attention items issue their cached K/V rows
-//     before they wait for q; the workgroups with attention items get no O
-//     rows, so h1 does not wait for the last merge;
+//   * a CU's vector memory operations complete in order, so a hand-over poll
+//     or result store waits for every load the CU issued before it; each
+//     layer's bytes are therefore placed in the windows where the CU would
+//     otherwise wait or compute, with only about a hand-over latency's worth
+//     ahead of each poll: during the layer-input and attention hand-overs each
+//     wave copies the first 4 gate/up pairs of its GU share (32 KiB) straight
+//     from HBM into LDS (buffer loads with the LDS bit), a few 1 KiB chunks
+//     per poll round; the O workgroups load 2 more gate/up pairs into
+//     registers before the attention-output wait; the first 8 KiB of each
+//     wave's down row are loaded during the gate/up dot products; attention
+//     items issue their cached K/V rows before they wait for q; the
+//     workgroups with attention items get no O rows, so h1 does not wait for
+//     the last merge;
 //   * GEMVs are bf16 x bf16 -> fp32 with v_dot2_f32_bf16, reduced across the
 //     wave with DPP row operations and four lane reads (bs=1 is
 //     bandwidth-bound: no MFMA);
@@ -97,17 +103,6 @@ static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
 #endif
 constexpr int D_EARLY = MK_D_EARLY;
 static_assert(D_EARLY >= 0 && D_EARLY <= 16, "down-projection early chunks");
-// The wave's first QKV row of the next layer loaded before the down-projection
-// dot products (1), and gate/up copy chunks issued when the layer input has
-// arrived, before the QKV dot products (MK_QKV_COPY), for the same reason.
-#ifndef MK_Q_EARLY
-#define MK_Q_EARLY 0
-#endif
-#ifndef MK_QKV_COPY
-#define MK_QKV_COPY 0
-#endif
-constexpr bool Q_EARLY = MK_Q_EARLY != 0;
-constexpr int QKV_COPY = MK_QKV_COPY;
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -366,12 +361,8 @@ __device__ __forceinline__ void qkv_rows(const Ctx& c, int li, rsrc_t& r, uint32
 // QKV phase of run-layer li: RMSNorm, GEMV, RoPE; q and the fresh K/V row to
 // the exchange buffer, the K/V row also into the caches. idle() runs between
 // the polls for the layer input.
-// qpre: the wave's first QKV row of this layer, already loaded when use_pre
-// (the ring then reads that row's chunks as zero). post() runs once the layer
-// input has arrived, before the dot products.
-template <class Idle, class Post>
-__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, const u32x4 (&qpre)[4], bool use_pre,
-                                          Post&& post) {
+template <class Idle>
+__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
   const KParams& p = *c.p;
   const int wave = wave_id();
   const int P0 = c.P0, P1 = c.P1;
@@ -380,13 +371,12 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, c
   int wn;
   qkv_rows(c, li, wr, woff, wn);
   RowStream<4, 4> rs;
-  rs.start(wr, woff, NWAVE * H * 2, wn, use_pre ? 4 : 0);
+  rs.start(wr, woff, NWAVE * H * 2, wn);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li == 0) stage_vec<1>(c.s, c.x_in, false, L.x);
   else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x, idle);
   lds_sync();
   trace_mark(c.s, 2 * xk(li, 1));
-  post();
   u32x4 xs[4];
   lds_x2048(L.x, xs);
   rmsnorm2048(xs, nullptr);
@@ -394,7 +384,6 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, c
   if (wn <= 4) {   // all rows in the ring: one transposed reduction
     float pt[4];
     rs.dots(dotf, pt);
-    if (use_pre) pt[0] += dot2048(qpre, xs);
     const float v = reduce_rows<4>(pt);
     const int r = lane_id() >> 4;
     if ((lane_id() & 15) == 0 && r < wn) L.val[wave + NWAVE * r] = v;
@@ -533,8 +522,6 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       share(INTER, G, w, U0, U1);
       c.gu_pairs = wave_span(U0, U1);
     }
-    u32x4 qpre[4];   // the next layer's first QKV row of the wave (Q_EARLY)
-    bool qpre_ok = false;
     for (int li = 0; li < p.n_layers; ++li) {
       const int l = p.first_layer + li;
       const bool last = li == p.n_layers - 1;
@@ -546,8 +533,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, c.gu_pairs, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
-      phase_qkv(c, li, L, gidle, qpre, qpre_ok, [&]() { gpf.issue_fixed<QKV_COPY>(L.spare); });
-      qpre_ok = false;
+      phase_qkv(c, li, L, gidle);
       if (li == 8) trace_value(c.s, 1, (unsigned long long)gpf.next);
       phase_attn(c, li, L);
 
@@ -691,16 +677,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         stage_vec<4>(c.s, c.xb(li, X_ACT), true, L.v);
         lds_sync();
         trace_mark(c.s, 2 * xk(li, 5));
-        if (Q_EARLY && li + 1 < p.n_layers && c.qkv_n <= 4) {
-          rsrc_t qr;
-          uint32_t qo;
-          int qn;
-          qkv_rows(c, li + 1, qr, qo, qn);
-          const uint32_t o = (qn > 0 ? qo : OOB) + (uint32_t)lane * 16u;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) qpre[i] = ld_stream(qr, o + (uint32_t)i * 1024u);
-          qpre_ok = true;
-        }
+
         uint16_t* h2 = c.xb(li, X_H2);
         u32x4 xs[16];
 #pragma unroll
