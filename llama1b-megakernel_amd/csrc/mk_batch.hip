@@ -384,6 +384,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
     __syncthreads();   // L.red reuse
   }
   arrive(c.ho(li, HO_QKV), c.w % N_SUB);
+  trace_done(c.s, li, 0);
 }
 
 // Attention: the workgroup's items (sequence, kv head, split); the last split
@@ -443,6 +444,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
     }
   }
+  if (waited) trace_done(c.s, li, 1);
 }
 
 // O projection (split-K, A = attention output read in MFMA layout) + residual -> h1.
@@ -481,6 +483,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
     __syncthreads();
   }
   arrive(c.ho(li, HO_H1), c.w % N_SUB);
+  trace_done(c.s, li, 2);
 }
 
 // RMSNorm(h1) -> gate/up GEMM (whole tiles per wave) -> silu(gate) * up -> act.
@@ -536,6 +539,7 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
     if (u + 1 < nunits) unit(u + 1, wb);
   }
   arrive(c.ho(li, HO_ACT), c.w % N_SUB);
+  trace_done(c.s, li, 3);
 }
 
 // Down projection (split-K over the waves, A = act read in MFMA layout) + residual -> h2.
@@ -602,6 +606,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
     if (u + 1 < nunits) unit(u + 1, ub);
   }
   arrive(c.ho(li, HO_H2), c.w % N_SUB);
+  trace_done(c.s, li, 4);
 }
 
 // Order-preserving 64-bit argmax key: larger value first, then lower index.

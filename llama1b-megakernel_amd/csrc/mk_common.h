@@ -509,6 +509,11 @@ __device__ __forceinline__ u32x4 rope_pair(float a, float b, const uint16_t* rro
 }
 
 
+template <bool V>
+struct BoolC {
+  static constexpr bool value = V;
+};
+
 // K/V rows of an attention item streamed ATT_GROUP at a time: thread t loads
 // row (t >> 3) of each 32-row round, dims (t & 7)*8 .. +7, of K and of V.
 // Rows >= jc read zero through OOB offsets and are flagged invalid.
@@ -612,11 +617,52 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
   // item read nothing: out-of-range offsets), so the compiler's wait before each consume counts
   // exactly the loads issued after it instead of falling back to waiting for all of them.
   const int ngroups = rows.ngroups();
+  // A full group (every row valid), the same arithmetic in the same order as
+  // consume(), as straight-line code: without the per-round checks and masks
+  // the compiler can interleave the 16 independent dot / softmax chains
+  // (with the checks the loop body was split into ~35 small blocks per group).
+  // MASKED: a partial group, every round computed with the invalid rows masked
+  // (score -inf, weight 0; their K/V read as zero) instead of skipping rounds
+  // with branches: the same results.
+  auto consume_full = [&](const AttnGroup& gr, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    float sc[ATT_R][GQA];
+#pragma unroll
+    for (int r = 0; r < ATT_R; ++r)
+#pragma unroll
+      for (int g = 0; g < GQA; ++g) {
+        const float x = sum_lanes8(dot8(gr.k[r], q[g], 0.f)) * SM_SCALE;
+        sc[r][g] = !MASKED || gr.valid[r] ? x : -INFINITY;
+      }
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      float mn = m_run[g];
+#pragma unroll
+      for (int r = 0; r < ATT_R; ++r) mn = fmaxf(mn, sc[r][g]);
+      const float keep = mn == -INFINITY ? 1.f : __expf(m_run[g] - mn);
+      l_run[g] *= keep;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
+#pragma unroll
+      for (int r = 0; r < ATT_R; ++r) {
+        const float pr = !MASKED || gr.valid[r] ? __expf(sc[r][g] - mn) : 0.f;
+        l_run[g] += pr;
+        const uint32_t w4[4] = {gr.v[r].x, gr.v[r].y, gr.v[r].z, gr.v[r].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[g][2 * e] = fmaf(pr, bf_lo(w4[e]), acc[g][2 * e]);
+          acc[g][2 * e + 1] = fmaf(pr, bf_hi(w4[e]), acc[g][2 * e + 1]);
+        }
+      }
+      m_run[g] = mn;
+    }
+  };
   auto step = [&](int gi, AttnGroup& cur, AttnGroup& ahead) {
     rows.load(gi + DEPTH, ahead);   // past the last group: all rows invalid, nothing read
     if (gi < ngroups) {
       const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
-      consume(cur.k, cur.v, cur.valid, left >= ATT_GROUP ? ATT_R : (left + 31) / 32);
+      if (left >= ATT_GROUP) consume_full(cur, BoolC<false>());
+      else consume_full(cur, BoolC<true>());
     }
   };
   AttnGroup& A = first;
