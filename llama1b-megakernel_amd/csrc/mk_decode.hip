@@ -78,10 +78,10 @@ constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM 
 // 1 KiB chunks of that copy issued per poll round of the layer-input wait and
 // of the attention-output wait
 #ifndef MK_GU_STEP_QKV
-#define MK_GU_STEP_QKV 6
+#define MK_GU_STEP_QKV 8
 #endif
 #ifndef MK_GU_STEP_O
-#define MK_GU_STEP_O 4
+#define MK_GU_STEP_O 6
 #endif
 constexpr int GU_LDS_STEP_QKV = MK_GU_STEP_QKV, GU_LDS_STEP_O = MK_GU_STEP_O;
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
