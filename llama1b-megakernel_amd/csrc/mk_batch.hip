@@ -51,6 +51,9 @@
 #ifndef MK_BATT_DEPTH
 #define MK_BATT_DEPTH 1
 #endif
+#ifndef MK_BGU_PRE
+#define MK_BGU_PRE 1
+#endif
 
 namespace {
 
@@ -216,9 +219,12 @@ __device__ __forceinline__ void load_a(rsrc_t r, int B, int row_elems, int k0, u
 //   xn = bf16(g * bf16(x * rsqrt(mean(x^2) + eps)))     (final norm, gamma g)
 // src: an exchange buffer or hidden_in (row b at b*4096 bytes), or the
 // embedding table (gather: row of token L.tok[b]).
+// The staging copies of stage_norm (issued by stage_issue), then the
+// normalisation (stage_finish). `after` runs between them: loads issued there
+// (a fixed count, AFTER of them) are not waited for, since vector loads
+// complete in order.
 template <int MT>
-__device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gather, const uint16_t* gamma, int r0,
-                                           int r1, BLds<MT>& L) {
+__device__ __forceinline__ void stage_issue(const BCtx& c, rsrc_t src, bool gather, BLds<MT>& L) {
   const int wave = wave_id(), lane = lane_id();
   // 1 KiB quarters of rows: wave w copies quarters w, w+4, ... (16*MT each)
 #pragma unroll
@@ -228,7 +234,27 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
     const uint32_t off = m < c.B ? row * (uint32_t)(H * 2) + (uint32_t)(qq * 1024 + lane * 16) : OOB;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr_t)&L.xn[m][qq * 512], 16, off, 0, 0, 0);
   }
-  wait_mem();
+  // no memory access may move above the copies: stage_finish counts on them
+  // being the oldest loads in flight
+  asm volatile("" ::: "memory");
+}
+template <int AFTER>
+__device__ __forceinline__ void wait_vm_after() {
+  static_assert(AFTER >= 0 && AFTER < 64, "vmcnt range");
+  // vmcnt(AFTER): bits 3:0 and 15:14; expcnt and lgkmcnt at their maxima (no wait)
+  __builtin_amdgcn_s_waitcnt((AFTER & 15) | ((AFTER >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+template <int MT, int AFTER = 0>
+__device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L);
+template <int MT>
+__device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gather, const uint16_t* gamma, int r0,
+                                           int r1, BLds<MT>& L) {
+  stage_issue<MT>(c, src, gather, L);
+  stage_finish<MT, 0>(c, gamma, r0, r1, L);
+}
+template <int MT, int AFTER>
+__device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
+  wait_vm_after<AFTER>();
   __syncthreads();
   // RMS per row: 16 threads (a 16-lane row of a wave) per token row, chunk q16 + 16i
   // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped
@@ -504,11 +530,16 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
                (u % UPT) * KS * 32, wv);
   };
   u32x4 wa[KS], wb[KS];
-  issue(0, wa);
-  issue(1, wb);
+  // MK_BGU_PRE weight units are issued before the h1 wait, the others right
+  // behind the h1 staging copies, so the staging does not queue behind them
+  if (MK_BGU_PRE >= 1) issue(0, wa);
+  if (MK_BGU_PRE >= 2) issue(1, wb);
   trace_mark(c.s, 2 * xk(li, 4) - 1);
   wait_grid(c, li, HO_H1);
-  stage_norm<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+  stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L);
+  if (MK_BGU_PRE < 1) issue(0, wa);
+  if (MK_BGU_PRE < 2) issue(1, wb);
+  stage_finish<MT, (2 - MK_BGU_PRE) * KS>(c, nullptr, R0, R1, L);
   trace_mark(c.s, 2 * xk(li, 4));
   uint16_t* act = c.xb(li, p.lay.act);
   f32x4 acc[MT];
