@@ -25,6 +25,13 @@ Their caches below each sequence's start position hold N(0,1) bf16 values
 instead of prefilled K/V (the step's cost does not depend on the values);
 tok/s counts every sequence's token.
 
+``--config c2`` times BASELINE config 2 instead: one decoder layer (layer 0 of
+the seed-0 weights) as its own launch of the decode kernel (``mk_layer_step``
+seam), batch 1, a 1024-row KV cache of N(0,1) bf16 values, the step at position
+1023 and an N(0,1) input row; it reports µs per layer launch and HBM GB/s, and
+its CPU baseline (the oracle's layer, timed on the host) doubles as the check:
+the max-abs error of the GPU layer against it.
+
 ``--gpus N`` with N > 1 exits: this benchmark runs on one GPU.
 """
 
@@ -99,8 +106,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=24)
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", choices=["c3", "c4", "c5"], default="c3",
-                    help="c3: the headline bs=1 decode; c4/c5: the batched configurations")
+    ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c3",
+                    help="c3: the headline bs=1 decode; c2: one decoder layer; c4/c5: the batched configurations")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 10 plain device copies of BYTES (HBM counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -116,6 +123,9 @@ def main():
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
+    if args.config == "c2":
+        run_layer(args)
+        return
     if args.config != "c3":
         run_batched(args, BATCH_CONFIGS[args.config])
         return
@@ -209,6 +219,90 @@ def main():
         from mk_weights import synthetic_state_dict
         sd = synthetic_state_dict(seed=0)
         result["cpu_baseline"] = cpu_baseline(sd, args.cpu_steps, args.cpu_budget_s)
+    print(json.dumps(result), flush=True)
+
+
+def run_layer(args):
+    """one decoder layer launch at KV position 1023."""
+    import torch
+    import mk_lib
+    from mk_config import LlamaDims, step_bytes
+    from mk_weights import pack_for_megakernel, synthetic_state_dict
+
+    S, POS = S_MAX, S_MAX - 1
+    dp = LlamaDims(n_layers=1)
+    sd = synthetic_state_dict(seed=0, d=dp)
+    packed = pack_for_megakernel(sd, dp, device="cuda", rope_rows=S)
+    w = mk_lib.weights_struct(packed)
+    g = torch.Generator().manual_seed(2)
+    hidden = torch.randn(1, 2048, generator=g).to(torch.bfloat16)
+    k0 = torch.randn(1, 8, S, 64, generator=g).to(torch.bfloat16)
+    v0 = torch.randn(1, 8, S, 64, generator=g).to(torch.bfloat16)
+    kc, vc = k0.cuda(), v0.cuda()
+    ws = mk_lib.Workspace(1, S, torch.device("cuda"))
+    pos = torch.tensor([POS], dtype=torch.int32, device="cuda")
+    out = torch.empty(1, 2048, dtype=torch.bfloat16, device="cuda")
+    step = mk_lib.StepLauncher(w, ws, [kc], [vc], pos, hidden_in=hidden.cuda(), hidden_out=out)
+    for _ in range(args.warmup):
+        step.launch()          # every launch recomputes the same layer (row POS rewritten identically)
+    torch.cuda.synchronize()
+    K = args.steps
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    evs[0].record()
+    for i in range(K):
+        step.launch()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    bits = ws.read_device_error()
+    if bits:
+        sys.exit(f"device error bits 0x{bits:x}")
+    us = [evs[i].elapsed_time(evs[i + 1]) * 1e3 for i in range(K)]
+    mean_us = sum(us) / K
+    nbytes = step_bytes(1, [POS], lm_head=False) + 2048 * 2   # + the hidden_out row
+    achieved = nbytes / (mean_us * 1e-6) / 1e9
+    result = {
+        "metric": "single decoder layer us per launch (Llama-3.2-1B layer, batch 1, KV length 1024); HBM GB/s",
+        "value": round(mean_us, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "p50_us": round(statistics.median(us), 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) bf16 layer weights seed 0, N(0,1) bf16 input and KV cache)",
+        "config": {"workload": "C2: one Llama-3.2-1B decoder layer as its own launch, batch 1, KV cache "
+                               f"[1,8,{S},64], step at position {POS}", "batch": 1, "kv_rows": S, "n_layers": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_step": int(nbytes),
+                     "kernel": "mk_decode_kernel (one layer, no lm_head)"},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        # the oracle's layer on the host cores: timed, and the reference for the max-abs check
+        from oracle.llama_ref import Dims, OracleLlama
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        torch.set_num_threads(threads)
+        o = OracleLlama(sd, Dims(n_layers=1), mode="mk")
+        times, ref = [], None
+        for _ in range(5):
+            cache = [(k0[0].float().clone(), v0[0].float().clone())]
+            t = time.perf_counter()
+            _, ref = o.forward(None, POS, cache, hidden=hidden.float(), want_logits=False)
+            times.append(time.perf_counter() - t)
+        err = (out.cpu().float() - ref).abs().max().item()
+        result["max_abs_err_vs_oracle"] = round(err, 5)
+        result["cpu_baseline"] = {
+            "value": round(statistics.median(times) * 1e6, 1), "unit": "us", "cores": threads, "kind": "port",
+            "sample": "5 runs of the oracle's decoder layer (fp32 accumulation, bf16 rounding points) at "
+                      f"position {POS}, median",
+        }
     print(json.dumps(result), flush=True)
 
 
