@@ -361,20 +361,29 @@ __device__ __forceinline__ void qkv_rows(const Ctx& c, int li, rsrc_t& r, uint32
 // QKV phase of run-layer li: RMSNorm, GEMV, RoPE; q and the fresh K/V row to
 // the exchange buffer, the K/V row also into the caches. idle() runs between
 // the polls for the layer input.
-template <class Idle>
-__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle) {
-  const KParams& p = *c.p;
-  const int wave = wave_id();
-  const int P0 = c.P0, P1 = c.P1;
+// The wave's QKV weight ring of run-layer li, issued (the caller issues it
+// before phase_qkv; the first layer's at kernel start).
+__device__ __forceinline__ void qkv_ring(const Ctx& c, int li, RowStream<4, 4>& rs) {
   rsrc_t wr;
   uint32_t woff;
   int wn;
   qkv_rows(c, li, wr, woff, wn);
-  RowStream<4, 4> rs;
   rs.start(wr, woff, NWAVE * H * 2, wn);
+}
+
+// rs: this layer's ring, already issued. pre_sync() runs just before the
+// workgroup barrier that follows the wait for the layer input.
+template <class Idle, class PreSync>
+__device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, RowStream<4, 4>& rs,
+                                          PreSync&& pre_sync) {
+  const KParams& p = *c.p;
+  const int wave = wave_id();
+  const int P0 = c.P0, P1 = c.P1;
+  const int wn = c.qkv_n;
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li == 0) stage_vec<1>(c.s, c.x_in, false, L.x);
   else stage_vec<1>(c.s, c.xb(li - 1, X_H2), true, L.x, idle);
+  pre_sync();
   lds_sync();
   trace_mark(c.s, 2 * xk(li, 1));
   u32x4 xs[4];
@@ -472,38 +481,45 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   trace_mark(c.s, 0);
   c.G = gridDim.x;
   c.w = blockIdx.x;
+  // The control words, the position and the token first; then the first
+  // layer's QKV weight ring (it depends on nothing), then the loads that need
+  // the position or the token, so that those wait only for the small loads.
   const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.pos = p.pos[0];
+  int tok = p.hidden_in ? 0 : p.tokens[0];
+  const int G = c.G, w = c.w, wave = wave_id(), lane = lane_id();
+  share(QKV_PAIRS, G, w, c.P0, c.P1);
+  c.qkv_n = wave_count(0, 2 * (c.P1 - c.P0));
+  RowStream<4, 4> qs;   // the QKV ring of the layer being run
+  qkv_ring(c, 0, qs);
   c.set = p.xch + (size_t)(epoch & 1u) * SET_BYTES;
-  {
-    // refill the other set with the sentinel for the next launch
+  // refill the other set with the sentinel for the next launch: during the
+  // lm_head phase, where the stores delay nothing, or here if there is none
+  auto refill = [&]() {
     u32x4* other = reinterpret_cast<u32x4*>(p.xch + (size_t)((epoch + 1u) & 1u) * SET_BYTES);
     const size_t n = SET_BYTES / 16;
     int lo, hi;
     share((int)n, c.G, c.w, lo, hi);
     for (int i = lo + threadIdx.x; i < hi; i += NT) other[i] = u32x4{~0u, ~0u, ~0u, ~0u};
-  }
-  c.pos = p.pos[0];
+  };
   const bool pos_ok = c.pos >= 0 && c.pos < p.s_max && c.pos < p.rope_rows;
+  if (!p.do_lm || !pos_ok) refill();   // (the lm_head phase runs only with a valid position)
   if (!pos_ok && blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   c.n_rows = c.pos + 1;
   if (p.hidden_in) {
     c.x_in = p.hidden_in;
   } else {
-    int tok = p.tokens[0];
     tok = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
     c.x_in = p.embed + (size_t)tok * H;
   }
-  const int G = c.G, w = c.w, wave = wave_id(), lane = lane_id();
-  if (pos_ok && threadIdx.x < HD)   // the step's RoPE row, read once
-    reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] =
-        reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
-  lds_sync();
+  // the step's RoPE row, read once; it goes to LDS with the first layer's input
+  uint32_t rope_v = 0;
+  if (pos_ok && threadIdx.x < HD)
+    rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
 
   if (pos_ok) {
     {
-      share(QKV_PAIRS, G, w, c.P0, c.P1);
-      c.qkv_n = wave_count(0, 2 * (c.P1 - c.P0));
       attn_split(c.n_rows, ATT_MAX_SPLIT, 32, c.nsplit, c.att_rows);
       int R0, R1;
       share(H, G, w, R0, R1);
@@ -533,7 +549,10 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       gpf.start(p.w_gu + (size_t)l * 2 * INTER * H, c.gu_pairs, L.gu[__builtin_amdgcn_readfirstlane(wave)]);
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
-      phase_qkv(c, li, L, gidle);
+      if (li > 0) qkv_ring(c, li, qs);
+      phase_qkv(c, li, L, gidle, qs, [&]() {
+        if (li == 0 && threadIdx.x < HD) reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] = rope_v;
+      });
       if (li == 8) trace_value(c.s, 1, (unsigned long long)gpf.next);
       phase_attn(c, li, L);
 
@@ -732,6 +751,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       stage_vec<1>(c.s, c.xb(p.n_layers - 1, X_H2), true, L.x);
       lds_sync();
       trace_mark(c.s, 2 * xk(p.n_layers, 1));
+      refill();
       u32x4 xs[4];
       lds_x2048(L.x, xs);
       rmsnorm2048(xs, p.g_final);
