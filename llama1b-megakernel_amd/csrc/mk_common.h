@@ -514,14 +514,17 @@ struct BoolC {
   static constexpr bool value = V;
 };
 
-// K/V rows of an attention item streamed ATT_GROUP at a time: thread t loads
-// row (t >> 3) of each 32-row round, dims (t & 7)*8 .. +7, of K and of V.
-// Rows >= jc read zero through OOB offsets and are flagged invalid.
+// K/V rows of an attention item streamed a group of R rounds of 32 rows at a
+// time (ATT_GROUP rows by default): thread t loads row (t >> 3) of each round,
+// dims (t & 7)*8 .. +7, of K and of V. Rows >= jc read zero through OOB
+// offsets and are flagged invalid.
 constexpr int ATT_R = ATT_GROUP / 32;
-struct AttnGroup {
-  u32x4 k[ATT_R], v[ATT_R];
-  bool valid[ATT_R];
+template <int R = ATT_R>
+struct AttnGroupT {
+  u32x4 k[R], v[R];
+  bool valid[R];
 };
+using AttnGroup = AttnGroupT<>;
 struct AttnRows {
   rsrc_t rk, rv;
   int j0, jc;
@@ -533,12 +536,14 @@ struct AttnRows {
     j0 = j0_;
     jc = jc_;
   }
-  __device__ __forceinline__ int ngroups() const { return jc > j0 ? (jc - j0 + ATT_GROUP - 1) / ATT_GROUP : 0; }
-  __device__ __forceinline__ void load(int gi, AttnGroup& g) const {
+  template <int R>
+  __device__ __forceinline__ int ngroups() const { return jc > j0 ? (jc - j0 + 32 * R - 1) / (32 * R) : 0; }
+  template <int R>
+  __device__ __forceinline__ void load(int gi, AttnGroupT<R>& g) const {
     const int rl = threadIdx.x >> 3, ch = threadIdx.x & 7;
 #pragma unroll
-    for (int r = 0; r < ATT_R; ++r) {
-      const int j = j0 + gi * ATT_GROUP + 32 * r + rl;
+    for (int r = 0; r < R; ++r) {
+      const int j = j0 + gi * 32 * R + 32 * r + rl;
       g.valid[r] = j < jc;
       const uint32_t off = g.valid[r] ? (uint32_t)(j * HD + ch * 8) * 2u : OOB;
       g.k[r] = ld_stream(rk, off);
@@ -557,9 +562,9 @@ struct AttnRows {
 // of it; rows stream in groups of ATT_GROUP with an online softmax, DEPTH
 // (1 or 2) groups ahead in flight. Writes the item's partial (m[4], l[4],
 // o[4][64]) unnormalised, relative to m.
-template <int DEPTH = 1>
-__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first, const uint16_t* q_lds, bool fresh,
-                                          float* part, AttnShared& sh) {
+template <int DEPTH = 1, int R = ATT_R>
+__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& first, const uint16_t* q_lds,
+                                          bool fresh, float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
   u32x4 q[GQA];
 #pragma unroll
@@ -572,13 +577,13 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
-  // consume rounds of 32 rows (R = rounds in the arrays, the first nr of them
+  // consume rounds of 32 rows (RA = rounds in the arrays, the first nr of them
   // holding any valid row): online softmax update
   auto consume = [&](const auto& kk, const auto& vv, const auto& valid, int nr) {
-    constexpr int R = sizeof(valid) / sizeof(valid[0]);
-    float sc[R][GQA];
+    constexpr int RA = sizeof(valid) / sizeof(valid[0]);
+    float sc[RA][GQA];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < RA; ++r)
 #pragma unroll
       for (int g = 0; g < GQA; ++g) {
         sc[r][g] = -INFINITY;
@@ -591,13 +596,13 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     for (int g = 0; g < GQA; ++g) {
       float mn = m_run[g];
 #pragma unroll
-      for (int r = 0; r < R; ++r) mn = fmaxf(mn, sc[r][g]);
+      for (int r = 0; r < RA; ++r) mn = fmaxf(mn, sc[r][g]);
       const float keep = mn == -INFINITY ? 1.f : __expf(m_run[g] - mn);
       l_run[g] *= keep;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
+      for (int r = 0; r < RA; ++r) {
         if (r >= nr) continue;
         const float pr = valid[r] ? __expf(sc[r][g] - mn) : 0.f;
         l_run[g] += pr;
@@ -611,12 +616,12 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
       m_run[g] = mn;
     }
   };
-  // cached rows in groups of ATT_GROUP, the loads of the next DEPTH groups in flight while one is
+  // cached rows in groups of R rounds, the loads of the next DEPTH groups in flight while one is
   // consumed. The buffers rotate by unrolling (a register copy of a buffer whose loads are in
   // flight would wait for them), and the loads ahead are issued unconditionally (rows past the
   // item read nothing: out-of-range offsets), so the compiler's wait before each consume counts
   // exactly the loads issued after it instead of falling back to waiting for all of them.
-  const int ngroups = rows.ngroups();
+  const int ngroups = rows.template ngroups<R>();
   // A full group (every row valid), the same arithmetic in the same order as
   // consume(), as straight-line code: without the per-round checks and masks
   // the compiler can interleave the 16 independent dot / softmax chains
@@ -624,11 +629,11 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
   // MASKED: a partial group, every round computed with the invalid rows masked
   // (score -inf, weight 0; their K/V read as zero) instead of skipping rounds
   // with branches: the same results.
-  auto consume_full = [&](const AttnGroup& gr, auto masked) {
+  auto consume_full = [&](const AttnGroupT<R>& gr, auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
-    float sc[ATT_R][GQA];
+    float sc[R][GQA];
 #pragma unroll
-    for (int r = 0; r < ATT_R; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int g = 0; g < GQA; ++g) {
         const float x = sum_lanes8(dot8(gr.k[r], q[g], 0.f)) * SM_SCALE;
@@ -638,13 +643,13 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
     for (int g = 0; g < GQA; ++g) {
       float mn = m_run[g];
 #pragma unroll
-      for (int r = 0; r < ATT_R; ++r) mn = fmaxf(mn, sc[r][g]);
+      for (int r = 0; r < R; ++r) mn = fmaxf(mn, sc[r][g]);
       const float keep = mn == -INFINITY ? 1.f : __expf(m_run[g] - mn);
       l_run[g] *= keep;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] *= keep;
 #pragma unroll
-      for (int r = 0; r < ATT_R; ++r) {
+      for (int r = 0; r < R; ++r) {
         const float pr = !MASKED || gr.valid[r] ? __expf(sc[r][g] - mn) : 0.f;
         l_run[g] += pr;
         const uint32_t w4[4] = {gr.v[r].x, gr.v[r].y, gr.v[r].z, gr.v[r].w};
@@ -657,23 +662,23 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroup& first
       m_run[g] = mn;
     }
   };
-  auto step = [&](int gi, AttnGroup& cur, AttnGroup& ahead) {
+  auto step = [&](int gi, AttnGroupT<R>& cur, AttnGroupT<R>& ahead) {
     rows.load(gi + DEPTH, ahead);   // past the last group: all rows invalid, nothing read
     if (gi < ngroups) {
-      const int left = rows.jc - rows.j0 - gi * ATT_GROUP;   // rows of this group and beyond
-      if (left >= ATT_GROUP) consume_full(cur, BoolC<false>());
+      const int left = rows.jc - rows.j0 - gi * 32 * R;   // rows of this group and beyond
+      if (left >= 32 * R) consume_full(cur, BoolC<false>());
       else consume_full(cur, BoolC<true>());
     }
   };
-  AttnGroup& A = first;
+  AttnGroupT<R>& A = first;
   if (DEPTH == 1) {
-    AttnGroup B;
+    AttnGroupT<R> B;
     for (int gi = 0; gi < ngroups; gi += 2) {
       step(gi, A, B);
       step(gi + 1, B, A);
     }
   } else {
-    AttnGroup B, C;
+    AttnGroupT<R> B, C;
     rows.load(1, B);
     for (int gi = 0; gi < ngroups; gi += 3) {
       step(gi, A, C);

@@ -73,7 +73,16 @@ namespace {
 
 using namespace mk;
 
-constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
+// KV-length splits per kv head (attention work items) and rounds of 32 rows
+// per attention group
+#ifndef MK_ATT_SPLITS
+#define MK_ATT_SPLITS 8
+#endif
+#ifndef MK_ATT_ROUNDS
+#define MK_ATT_ROUNDS 4
+#endif
+constexpr int ATT_MAX_SPLIT = MK_ATT_SPLITS;
+constexpr int ATT_RD = MK_ATT_ROUNDS;
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
 // 1 KiB chunks of that copy issued per poll round of the layer-input wait and
 // of the attention-output wait
@@ -444,7 +453,7 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     AttnRows ar;
     ar.init(c.p->kc[li] + (size_t)h * c.p->s_max * HD, c.p->vc[li] + (size_t)h * c.p->s_max * HD, c.p->s_max, j0,
             min(j1, c.pos));
-    AttnGroup g0;
+    AttnGroupT<ATT_RD> g0;
     ar.load(0, g0);
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2) - 1);
     if (wave_id() == 0) {
