@@ -20,15 +20,18 @@ constexpr int BATT_MAX_SPLIT = 16;  // KV-length splits per (sequence, kv head)
 //                     alternating by epoch; each launch zeroes the other set):
 //     hand-over counters [MK_MAX_LAYERS][5 hand-overs][8 sub-counters], one 128-byte line each
 //     attention-split counters u32 [MK_MAX_LAYERS][M][8 kv heads]
+//     down-projection row-group counters u32 [MK_MAX_LAYERS][DN_MAX]
 constexpr size_t BWS_KEY0 = 256;
 constexpr size_t BWS_KEY_STRIDE = 256;
 constexpr int N_HANDOVER = 5;   // per layer: qkv, att, h1, act, h2
 constexpr int N_SUB = 8;        // sub-counters per hand-over (arrivals spread over 8 lines)
 constexpr size_t CNT_LINE = 128;
 constexpr size_t HCNT_BYTES = (size_t)MK_MAX_LAYERS * N_HANDOVER * N_SUB * CNT_LINE;
+constexpr int DN_MAX = 256;     // row groups of the 2-D down projection (grid / 4) at most
+constexpr int DN_KQ = 4;        // K quarters of the 2-D down projection
 __host__ __device__ inline size_t bws_cnt0(int M) { return BWS_KEY0 + (size_t)M * BWS_KEY_STRIDE; }
 __host__ __device__ inline size_t bws_cnt_set(int M) {
-  return HCNT_BYTES + (size_t)MK_MAX_LAYERS * M * MK_N_KV_HEADS * 4;
+  return HCNT_BYTES + (size_t)MK_MAX_LAYERS * M * MK_N_KV_HEADS * 4 + (size_t)MK_MAX_LAYERS * DN_MAX * 4;
 }
 __host__ __device__ inline size_t batch_ws_bytes(int M) { return bws_cnt0(M) + 2 * bws_cnt_set(M); }
 // Largest batch a workspace of `bytes` serves with the batched layout (< 2: batch-1 layout).
@@ -47,12 +50,14 @@ inline int batch_of_ws_bytes(size_t bytes) {
 //   act  bf16 [M][8192]   silu(gate) * up
 //   h2   bf16 [M][2048]   layer output
 // and, after all layers, the attention partials
-//   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)].
+//   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)]
+// and the down-projection partials of the four K quarters
+//   dpart fp32 [layer][4][M][2048].
 // Every buffer is written once per launch and read only after its arrival
 // counter is complete.
 struct BatchLayout {
   size_t qkv, att, h1, act, h2, layer;   // within a layer
-  size_t part_base, part_layer, total;
+  size_t part_base, part_layer, dpart_base, dpart_layer, total;
   static constexpr size_t r256(size_t x) { return (x + 255) / 256 * 256; }
   void init(int M) {
     qkv = 0;
@@ -63,7 +68,9 @@ struct BatchLayout {
     layer = r256(h2 + (size_t)M * MK_HIDDEN * 2);
     part_base = (size_t)MK_MAX_LAYERS * layer;
     part_layer = r256((size_t)M * MK_N_KV_HEADS * BATT_MAX_SPLIT * 4 * (MK_HEAD_DIM + 2) * 4);
-    total = part_base + (size_t)MK_MAX_LAYERS * part_layer;
+    dpart_base = part_base + (size_t)MK_MAX_LAYERS * part_layer;
+    dpart_layer = r256((size_t)DN_KQ * M * MK_HIDDEN * 4);
+    total = dpart_base + (size_t)MK_MAX_LAYERS * dpart_layer;
   }
 };
 

@@ -54,6 +54,9 @@
 #ifndef MK_BGU_PRE
 #define MK_BGU_PRE 1
 #endif
+#ifndef MK_BDOWN_2D
+#define MK_BDOWN_2D 1
+#endif
 
 namespace {
 
@@ -134,12 +137,21 @@ struct BCtx {
   __device__ __forceinline__ int cache_seq(int b) const { return prefill ? 0 : b; }
   uint8_t* hcnt;    // this launch's hand-over counters [layer][5][8 lines]
   uint32_t* acnt;   // this launch's attention-split counters [layer][M][8]
+  uint32_t* dcnt;   // this launch's down-projection row-group counters [layer][DN_MAX]
+  // 2-D down projection (batches above 16): workgroup w computes rows
+  // [n*drpg, (n+1)*drpg), n = w / 4, over the K quarter w % 4 (needs grid % 4 == 0
+  // and whole 16-row tiles per group)
+  bool d2;
+  int dng, drpg;
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
     return reinterpret_cast<uint16_t*>(p->xch + (size_t)li * p->lay.layer + off);
   }
   __device__ __forceinline__ float* part(int li, int b, int h, int sp) const {
     return reinterpret_cast<float*>(p->xch + p->lay.part_base + (size_t)li * p->lay.part_layer) +
            ((size_t)(b * NKV + h) * BATT_MAX_SPLIT + sp) * PART_FLOATS;
+  }
+  __device__ __forceinline__ float* dpart(int li) const {
+    return reinterpret_cast<float*>(p->xch + p->lay.dpart_base + (size_t)li * p->lay.dpart_layer);
   }
   __device__ __forceinline__ uint32_t* ho(int li, int k) const {
     return reinterpret_cast<uint32_t*>(hcnt + ((size_t)li * N_HANDOVER + k) * N_SUB * CNT_LINE);
@@ -179,6 +191,12 @@ __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho
 // A hand-over produced by every workgroup of the grid (workgroup w adds to sub-counter w % 8).
 __device__ __forceinline__ void wait_grid(const BCtx& c, int li, int k) {
   wait_handover(c.s, c.ho(li, k), c.G / N_SUB, c.G % N_SUB);
+}
+// The h2 hand-over: from every workgroup, or with the 2-D down projection from
+// the one workgroup per row group n that sums its K quarters (sub-counter n % 8).
+__device__ __forceinline__ void wait_h2(const BCtx& c, int li) {
+  if (c.d2) wait_handover(c.s, c.ho(li, HO_H2), c.dng / N_SUB, c.dng % N_SUB);
+  else wait_grid(c, li, HO_H2);
 }
 
 // ---------------------------------------------------------------------------
@@ -357,7 +375,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
   load_w<KS>(rw, ntile > 0 ? row0 : row_end, row_end, H * 2, wave * KQ, wv);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li > 0) {
-    wait_grid(c, li - 1, HO_H2);
+    wait_h2(c, li - 1);
     stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
   } else if (p.hidden_in) {
     stage_norm<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
@@ -539,7 +557,9 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
   stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L);
   if (MK_BGU_PRE < 1) issue(0, wa);
   if (MK_BGU_PRE < 2) issue(1, wb);
-  stage_finish<MT, (2 - MK_BGU_PRE) * KS>(c, nullptr, R0, R1, L);
+  // the raw columns kept for the down projection's residual: its rows
+  const int D0 = c.d2 ? (c.w / DN_KQ) * c.drpg : R0, D1 = c.d2 ? D0 + c.drpg : R1;
+  stage_finish<MT, (2 - MK_BGU_PRE) * KS>(c, nullptr, D0, D1, L);
   trace_mark(c.s, 2 * xk(li, 4));
   uint16_t* act = c.xb(li, p.lay.act);
   f32x4 acc[MT];
@@ -640,6 +660,97 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
   trace_done(c.s, li, 4);
 }
 
+// Down projection as a 2-D split: workgroup w computes the rows of row group
+// n = w / 4 over the K quarter kq = w % 4 (split over the 4 waves as above), so
+// it reads a quarter of act instead of all of it and fills whole 16-row tiles.
+// The four quarters' fp32 partials go to dpart; the workgroup that completes a
+// row group last (an arrival counter) sums them in the fixed order kq = 0..3,
+// adds the residual and publishes the rows of h2.
+template <int MT>
+__device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id(), t = threadIdx.x;
+  const bool last = li == p.n_layers - 1;
+  const int n = c.w / DN_KQ, kq = c.w % DN_KQ;
+  const int R0 = n * c.drpg, R1 = R0 + c.drpg, ntile = c.drpg / 16;
+  constexpr int KW = INTER / DN_KQ / NWAVE;   // 512 columns per wave
+  constexpr int UPT = KW / (DKS * 32);         // 2 units per tile
+  const int nunits = ntile * UPT;
+  const int k0w = kq * (INTER / DN_KQ) + wave * KW;
+  const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
+  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)c.B * INTER * 2);
+  float* dp = c.dpart(li);
+  struct Unit {
+    u32x4 w[DKS];
+    u32x4 a[MT * DKS];
+  };
+  auto issue_w = [&](int u, Unit& un) {
+    load_w<DKS>(rw, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, k0w + (u % UPT) * DKS * 32, un.w);
+  };
+  auto issue_a = [&](int u, Unit& un) {
+    load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, k0w + (u % UPT) * DKS * 32, un.a);
+  };
+  Unit ua, ub;
+  issue_w(0, ua);
+  issue_w(1, ub);
+  trace_mark(c.s, 2 * xk(li, 5) - 1);
+  wait_grid(c, li, HO_ACT);
+  trace_mark(c.s, 2 * xk(li, 5));
+  issue_a(0, ua);
+  issue_a(1, ub);
+  f32x4 acc[MT];
+  auto unit = [&](int u, Unit& un) {
+    if (u % UPT == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    mma_reg<MT, DKS>(un.a, un.w, acc);
+    issue_w(u + 2, un);
+    issue_a(u + 2, un);
+    if (u % UPT == UPT - 1) {
+      const f32x4 d = reduce_waves<MT>(acc, L);
+      if (wave < MT) {
+        const int row = R0 + (u / UPT) * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = wave * 16 + (lane >> 4) * 4 + i;
+          if (m < c.B) st_dev(dp + ((size_t)kq * p.max_batch + m) * H + row, d[i]);
+        }
+      }
+      __syncthreads();
+    }
+  };
+  for (int u = 0; u < nunits; u += 2) {
+    unit(u, ua);
+    if (u + 1 < nunits) unit(u + 1, ub);
+  }
+  // count this quarter in; the row group's last quarter sums the four
+  wait_mem();
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(c.dcnt + (size_t)li * DN_MAX + n, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    L.flag = prev == (uint32_t)(DN_KQ - 1);
+  }
+  __syncthreads();
+  if (L.flag) {
+    const rsrc_t rp = make_rsrc(dp, (size_t)DN_KQ * p.max_batch * H * 4);
+    uint16_t* h2 = c.xb(li, p.lay.h2);
+    for (int i = t; i < c.B * c.drpg; i += NT) {
+      const int m = i / c.drpg, r = i % c.drpg, row = R0 + r;
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < DN_KQ; ++q)
+        sum += __uint_as_float(ld_dev4(rp, (uint32_t)((((size_t)q * p.max_batch + m) * H + row) * 4)));
+      const uint32_t hv = f2bf(bf2f(L.res[m][r]) + rbf(sum));
+      st_dev(h2 + (size_t)m * H + row, hv);
+      if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
+    }
+    arrive(c.ho(li, HO_H2), n % N_SUB);
+  }
+  trace_done(c.s, li, 4);
+}
+
 // Order-preserving 64-bit argmax key: larger value first, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
@@ -667,7 +778,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
   issue(0, wa);
   issue(1, wb);
   trace_mark(c.s, 2 * xk(p.n_layers, 1) - 1);
-  wait_grid(c, p.n_layers - 1, HO_H2);
+  wait_h2(c, p.n_layers - 1);
   stage_norm<MT>(c, make_rsrc(c.xb(p.n_layers - 1, p.lay.h2), (size_t)c.B * H * 2), false, p.g_final, R0, R1, L);
   trace_mark(c.s, 2 * xk(p.n_layers, 1));
   f32x4 acc[MT];
@@ -756,6 +867,12 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   uint8_t* cnt0 = p.ws + bws_cnt0(p.max_batch);
   c.hcnt = cnt0 + (size_t)(epoch & 1u) * cset;
   c.acnt = reinterpret_cast<uint32_t*>(c.hcnt + HCNT_BYTES);
+  c.dcnt = c.acnt + (size_t)MK_MAX_LAYERS * p.max_batch * NKV;
+  c.dng = c.G / DN_KQ;
+  c.drpg = c.dng > 0 ? H / c.dng : 0;
+  // (batch 8 measured slower with it: there act is small and the extra hand-over costs more)
+  c.d2 = MK_BDOWN_2D && MT == 2 && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
+         c.drpg <= RES_MAX;
   {
     // zero the other counter set for the next launch
     uint32_t* oc = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
@@ -851,7 +968,8 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
       phase_attn<MT>(c, li, L);
       phase_o<MT>(c, li, L);
       phase_gu<MT>(c, li, L);
-      phase_down<MT>(c, li, L);
+      if (c.d2) phase_down2d<MT>(c, li, L);
+      else phase_down<MT>(c, li, L);
     }
     if (p.do_lm) phase_lm<MT>(c, L);
   }
