@@ -275,25 +275,26 @@ __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamm
   wait_vm_after<AFTER>();
   __syncthreads();
   // RMS per row: 16 threads (a 16-lane row of a wave) per token row, chunk q16 + 16i
-  // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped
+  // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped.
+  // The sum of squares reads the row's 16 chunks with all loads in flight at
+  // once and sums with v_dot2 into two accumulators; the normalisation reads
+  // them again, four chunks at a time (the registers of a whole row would not
+  // fit next to the weight units in flight).
   const int q16 = threadIdx.x & 15;
   for (int m = threadIdx.x >> 4; m < c.B; m += NT / 16) {
-    float ss = 0.f;
-#pragma unroll 4
-    for (int i = 0; i < 16; ++i) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * i) * 8]);
-      const uint32_t e[4] = {x.x, x.y, x.z, x.w};
+    float ssa = 0.f, ssb = 0.f;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float a = bf_lo(e[k]), b = bf_hi(e[k]);
-        ss = fmaf(a, a, ss);
-        ss = fmaf(b, b, ss);
-      }
+    for (int i = 0; i < 16; i += 2) {
+      const u32x4 xa = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * i) * 8]);
+      const u32x4 xb = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * (i + 1)) * 8]);
+      ssa = dot8(xa, xa, ssa);
+      ssb = dot8(xb, xb, ssb);
     }
+    float ss = ssa + ssb;
     ss = sum_lanes8(ss);
     ss += dpp<DPP_ROR8>(ss);   // the 16 lanes of the row
     const float inv = rsqrtf(ss * (1.0f / H) + EPS);
-#pragma unroll 2
+#pragma unroll 4
     for (int i = 0; i < 16; ++i) {
       const int col = (q16 + 16 * i) * 8;
       const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][col]);
