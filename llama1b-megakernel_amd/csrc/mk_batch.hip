@@ -276,34 +276,32 @@ __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamm
   __syncthreads();
   // RMS per row: 16 threads (a 16-lane row of a wave) per token row, chunk q16 + 16i
   // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped.
-  // The sum of squares reads the row's 16 chunks with all loads in flight at
-  // once and sums with v_dot2 into two accumulators; the normalisation reads
-  // them again, four chunks at a time (the registers of a whole row would not
-  // fit next to the weight units in flight).
+  // The lanes of a row first copy its raw columns [r0, r1) to L.res (a wave's
+  // LDS accesses complete in order, so before any lane overwrites them), then
+  // read their 16 chunks into registers at once, sum the squares with v_dot2
+  // into two accumulators and write the normalised chunks back from the same
+  // registers: one LDS read and one write per chunk, no branch in the loop.
   const int q16 = threadIdx.x & 15;
   for (int m = threadIdx.x >> 4; m < c.B; m += NT / 16) {
+    uint16_t* row = &L.xn[m][0];
+    for (int col = r0 + q16; col < r1; col += 16) L.res[m][col - r0] = row[col];
+    u32x4 x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = *reinterpret_cast<const u32x4*>(&row[(q16 + 16 * i) * 8]);
     float ssa = 0.f, ssb = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const u32x4 xa = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * i) * 8]);
-      const u32x4 xb = *reinterpret_cast<const u32x4*>(&L.xn[m][(q16 + 16 * (i + 1)) * 8]);
-      ssa = dot8(xa, xa, ssa);
-      ssb = dot8(xb, xb, ssb);
+      ssa = dot8(x[i], x[i], ssa);
+      ssb = dot8(x[i + 1], x[i + 1], ssb);
     }
     float ss = ssa + ssb;
     ss = sum_lanes8(ss);
     ss += dpp<DPP_ROR8>(ss);   // the 16 lanes of the row
     const float inv = rsqrtf(ss * (1.0f / H) + EPS);
-#pragma unroll 4
+#pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int col = (q16 + 16 * i) * 8;
-      const u32x4 x = *reinterpret_cast<const u32x4*>(&L.xn[m][col]);
-      uint32_t e[4] = {x.x, x.y, x.z, x.w};
-      if (col + 8 > r0 && col < r1) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (col + q >= r0 && col + q < r1) L.res[m][col + q - r0] = (uint16_t)(e[q >> 1] >> (16 * (q & 1)));
-      }
+      uint32_t e[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
       u32x4 gv = {0u, 0u, 0u, 0u};
       if (gamma) gv = *reinterpret_cast<const u32x4*>(gamma + col);
       const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
@@ -312,7 +310,7 @@ __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamm
         const uint32_t n = cvt_bf2(bf_lo(e[k]) * inv, bf_hi(e[k]) * inv);
         e[k] = gamma ? cvt_bf2(bf_lo(g[k]) * bf_lo(n), bf_hi(g[k]) * bf_hi(n)) : n;
       }
-      *reinterpret_cast<u32x4*>(&L.xn[m][col]) = u32x4{e[0], e[1], e[2], e[3]};
+      *reinterpret_cast<u32x4*>(&row[col]) = u32x4{e[0], e[1], e[2], e[3]};
     }
   }
   __syncthreads();
