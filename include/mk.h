@@ -106,6 +106,24 @@ typedef struct mk_weights {
     const void *rope;
     int32_t n_layers;    /* layers present in the stacks (1..16)       */
     int32_t rope_rows;   /* rows of the rope table (>= s_max)          */
+    /*
+     * Optional second copies of w_qkv, w_o, w_gu, w_down and embed in MFMA
+     * tile order, read by the batched kernel (batch > 1 and prefill steps)
+     * when all five are set; NULL: it reads the row-major stacks above. For
+     * a matrix [N][K] (N a multiple of 16, K of 32) the 1 KiB block
+     * (n16, ks) = (row / 16, column / 32) sits at block index n16*(K/32) + ks,
+     * and in it the 16 bytes at ((column % 32) / 8 * 16 + row % 16) * 16 hold
+     * columns 8*j .. 8*j+7 of the k-step: one block is one MFMA B operand
+     * (16 rows x 32 columns), so each load instruction reads 1 KiB
+     * contiguous instead of 64 bytes from each of 16 rows. Stacked per layer
+     * like the row-major copies (same sizes). No counterpart in the reference
+     * (its NKI kernel has one layout per weight).
+     */
+    const void *t_qkv;
+    const void *t_o;
+    const void *t_gu;
+    const void *t_down;
+    const void *t_embed;
 } mk_weights;
 
 /*

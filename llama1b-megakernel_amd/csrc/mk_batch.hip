@@ -87,6 +87,8 @@ struct BParams {
   const uint16_t* w_gu;
   const uint16_t* w_d;
   const uint16_t* embed;
+  const uint16_t* lm;   // the lm_head rows: embed, or its tiled copy
+  int tiled;            // w_qkv, w_o, w_gu, w_d and lm are the tiled copies
   const uint16_t* g_final;
   const uint16_t* rope;
   uint16_t* kc[MK_MAX_LAYERS];
@@ -205,14 +207,27 @@ __device__ __forceinline__ void wait_h2(const BCtx& c, int li) {
 
 // The B-operand pieces of one weight unit of N k-steps: lane l holds row
 // row + l%16 (rows >= row_end read zero without a memory access) at columns
-// k0 + s*32 + (l/16)*8 .. +7 for k-step s.
+// k0 + s*32 + (l/16)*8 .. +7 for k-step s (k0 a multiple of 32).
+// Row-major matrices: each load reads 64 bytes from each of 16 rows.
+// Tiled matrices (1 KiB block per 16 rows x 32 columns, lane order inside):
+// each load reads one block, contiguous (streams ~20% faster).
 template <int N>
-__device__ __forceinline__ void load_w(rsrc_t r, int row, int row_end, uint32_t row_bytes, int k0, u32x4 (&wv)[N]) {
+__device__ __forceinline__ void load_w(rsrc_t r, bool tiled, int row, int row_end, uint32_t row_bytes, int k0,
+                                       u32x4 (&wv)[N]) {
   const int lane = lane_id();
   const int n = row + (lane & 15);
-  const uint32_t o = n < row_end ? (uint32_t)n * row_bytes + (uint32_t)(k0 + (lane >> 4) * 8) * 2u : OOB;
+  uint32_t o, step;
+  if (tiled) {
+    const uint32_t kb = row_bytes / 64u;   // k-steps (blocks) per 16-row tile
+    o = (((uint32_t)n >> 4) * kb + ((uint32_t)k0 >> 5)) * 1024u + (uint32_t)(lane >> 4) * 256u + (uint32_t)(n & 15) * 16u;
+    step = 1024u;
+  } else {
+    o = (uint32_t)n * row_bytes + (uint32_t)(k0 + (lane >> 4) * 8) * 2u;
+    step = 64u;
+  }
+  if (n >= row_end) o = OOB;
 #pragma unroll
-  for (int s = 0; s < N; ++s) wv[s] = ld_stream(r, o + (uint32_t)s * 64u);
+  for (int s = 0; s < N; ++s) wv[s] = ld_stream(r, o + (uint32_t)s * step);
 }
 
 // The A-operand pieces of N k-steps read straight from an exchange matrix
@@ -371,7 +386,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
   const int row0 = 2 * P0, row_end = 2 * P1, ntile = (row_end - row0 + 15) / 16;
   const rsrc_t rw = make_rsrc(p.w_qkv + (size_t)l * QKV_ROWS * H, QKV_LAYER_BYTES);
   u32x4 wv[KS];
-  load_w<KS>(rw, ntile > 0 ? row0 : row_end, row_end, H * 2, wave * KQ, wv);
+  load_w<KS>(rw, p.tiled, ntile > 0 ? row0 : row_end, row_end, H * 2, wave * KQ, wv);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (li > 0) {
     wait_h2(c, li - 1);
@@ -388,7 +403,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mma_lds<MT>(L, wave * KQ, wv, acc);
-    if (tt + 1 < ntile) load_w<KS>(rw, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
+    if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
     const f32x4 d = reduce_waves<MT>(acc, L);
     if (wave < MT) {
       const int row = row0 + tt * 16 + (lane & 15);
@@ -500,7 +515,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
   const int ntile = (R1 - R0 + 15) / 16;
   const rsrc_t rw = make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES);
   u32x4 wv[KS];
-  load_w<KS>(rw, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
+  load_w<KS>(rw, p.tiled, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
   trace_mark(c.s, 2 * xk(li, 3) - 1);
   // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % 8: B arrivals each
   wait_handover(c.s, c.ho(li, HO_ATT), c.B, 0);
@@ -513,7 +528,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mma_reg<MT, KS>(a, wv, acc);
-    if (tt + 1 < ntile) load_w<KS>(rw, R0 + 16 * (tt + 1), R1, H * 2, wave * KQ, wv);
+    if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, R0 + 16 * (tt + 1), R1, H * 2, wave * KQ, wv);
     const f32x4 d = reduce_waves<MT>(acc, L);
     if (wave < MT) {
       const int row = R0 + tt * 16 + (lane & 15);
@@ -543,7 +558,7 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
   const int nunits = my_tiles * UPT;
   const rsrc_t rw = make_rsrc(p.w_gu + (size_t)l * 2 * INTER * H, GU_LAYER_BYTES);
   auto issue = [&](int u, u32x4(&wv)[KS]) {
-    load_w<KS>(rw, u < nunits ? row0 + 16 * (wave + NWAVE * (u / UPT)) : row_end, row_end, H * 2,
+    load_w<KS>(rw, p.tiled, u < nunits ? row0 + 16 * (wave + NWAVE * (u / UPT)) : row_end, row_end, H * 2,
                (u % UPT) * KS * 32, wv);
   };
   u32x4 wa[KS], wb[KS];
@@ -611,7 +626,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
     u32x4 a[MT * DKS];
   };
   auto issue_w = [&](int u, Unit& un) {
-    load_w<DKS>(rw, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, wave * KW + (u % UPT) * DKS * 32, un.w);
+    load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, wave * KW + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
     load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, wave * KW + (u % UPT) * DKS * 32, un.a);
@@ -684,7 +699,7 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
     u32x4 a[MT * DKS];
   };
   auto issue_w = [&](int u, Unit& un) {
-    load_w<DKS>(rw, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, k0w + (u % UPT) * DKS * 32, un.w);
+    load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, k0w + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
     load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, k0w + (u % UPT) * DKS * 32, un.a);
@@ -769,9 +784,9 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
   constexpr int UPT = H / (KS * 32);
   const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
   const int nunits = my_tiles * UPT;
-  const rsrc_t rw = make_rsrc(p.embed, EMBED_BYTES);
+  const rsrc_t rw = make_rsrc(p.lm, EMBED_BYTES);
   auto issue = [&](int u, u32x4(&wv)[KS]) {
-    load_w<KS>(rw, u < nunits ? V0 + 16 * (wave + NWAVE * (u / UPT)) : V1, V1, H * 2, (u % UPT) * KS * 32, wv);
+    load_w<KS>(rw, p.tiled, u < nunits ? V0 + 16 * (wave + NWAVE * (u / UPT)) : V1, V1, H * 2, (u % UPT) * KS * 32, wv);
   };
   u32x4 wa[KS], wb[KS];
   issue(0, wa);
@@ -1050,6 +1065,15 @@ hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch
   kp.w_gu = static_cast<const uint16_t*>(w->w_gu);
   kp.w_d = static_cast<const uint16_t*>(w->w_down);
   kp.embed = static_cast<const uint16_t*>(w->embed);
+  kp.lm = kp.embed;
+  if (w->t_qkv && w->t_o && w->t_gu && w->t_down && w->t_embed) {
+    kp.tiled = 1;
+    kp.w_qkv = static_cast<const uint16_t*>(w->t_qkv);
+    kp.w_o = static_cast<const uint16_t*>(w->t_o);
+    kp.w_gu = static_cast<const uint16_t*>(w->t_gu);
+    kp.w_d = static_cast<const uint16_t*>(w->t_down);
+    kp.lm = static_cast<const uint16_t*>(w->t_embed);
+  }
   kp.g_final = static_cast<const uint16_t*>(w->norm_final);
   kp.rope = static_cast<const uint16_t*>(w->rope);
   for (int i = 0; i < a->n_layers; ++i) {

@@ -39,7 +39,11 @@ class MkWeights(ctypes.Structure):
         ("w_qkv", c_void_p), ("w_o", c_void_p), ("w_gu", c_void_p), ("w_down", c_void_p),
         ("embed", c_void_p), ("norm_final", c_void_p), ("rope", c_void_p),
         ("n_layers", c_int32), ("rope_rows", c_int32),
+        ("t_qkv", c_void_p), ("t_o", c_void_p), ("t_gu", c_void_p), ("t_down", c_void_p), ("t_embed", c_void_p),
     ]
+
+
+TILED_KEYS = {"t_qkv": "w_qkv", "t_o": "w_o", "t_gu": "w_gu", "t_down": "w_down", "t_embed": "embed"}
 
 
 class MkStepArgs(ctypes.Structure):
@@ -117,16 +121,26 @@ def current_stream_ptr() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def weights_struct(packed: Dict[str, torch.Tensor]) -> MkWeights:
-    """MkWeights view of ``mk_weights.pack_for_megakernel`` output (device tensors)."""
+def weights_struct(packed: Dict[str, torch.Tensor], tiled: bool = True) -> MkWeights:
+    """MkWeights view of ``mk_weights.pack_for_megakernel`` output (device tensors).
+    The MFMA-tiled copies (``t_*``, read by the batched kernel) are passed when
+    all five are present and ``tiled`` is true; otherwise the batched kernel
+    reads the row-major stacks."""
     for k in ("w_qkv", "w_o", "w_gu", "w_down", "embed", "norm_final", "rope"):
         t = packed[k]
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError(f"{k} must be contiguous bf16")
+    t_ptrs = [None] * 5
+    if tiled and all(k in packed for k in TILED_KEYS):
+        for k, src in TILED_KEYS.items():
+            t = packed[k]
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != packed[src].numel():
+                raise ValueError(f"{k} must be a contiguous bf16 tiling of {src}")
+        t_ptrs = [_ptr(packed[k]) for k in TILED_KEYS]
     return MkWeights(
         _ptr(packed["w_qkv"]), _ptr(packed["w_o"]), _ptr(packed["w_gu"]), _ptr(packed["w_down"]),
         _ptr(packed["embed"]), _ptr(packed["norm_final"]), _ptr(packed["rope"]),
-        int(packed["w_qkv"].shape[0]), int(packed["rope"].shape[0]))
+        int(packed["w_qkv"].shape[0]), int(packed["rope"].shape[0]), *t_ptrs)
 
 
 class Workspace:

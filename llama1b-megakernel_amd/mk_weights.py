@@ -38,7 +38,7 @@ from __future__ import annotations
 import concurrent.futures as _futures
 import math
 import os
-from typing import Dict, Iterable, List, Tuple
+from typing import Dict, Iterable, List, Optional, Tuple
 
 import torch
 
@@ -178,12 +178,29 @@ def pack_layer(sd: Dict[str, torch.Tensor], l: int, d: LlamaDims = LLAMA_3_2_1B,
     }
 
 
+def mfma_tiles(w: torch.Tensor) -> torch.Tensor:
+    """The MFMA tile order of a row-major bf16 matrix (or stack) [..., N, K]
+    (N % 16 == 0, K % 32 == 0) that the batched kernel reads: for each 16-row
+    tile and 32-column k-step a 1 KiB block, in it the 8 columns 8j..8j+7 of
+    row r at 16-byte slot j*16 + r (the B operand of one
+    v_mfma_f32_16x16x32_bf16, lane = slot). Same number of elements."""
+    *lead, n, k = w.shape
+    if n % 16 or k % 32:
+        raise ValueError(f"cannot tile a [{n}, {k}] matrix (rows % 16, columns % 32)")
+    t = w.reshape(*lead, n // 16, 16, k // 32, 4, 8)
+    nd = len(lead)
+    perm = list(range(nd)) + [nd, nd + 2, nd + 3, nd + 1, nd + 4]
+    return t.permute(*perm).contiguous().reshape(w.shape)
+
+
 def pack_for_megakernel(sd: Dict[str, torch.Tensor], d: LlamaDims = LLAMA_3_2_1B,
                         device: str | torch.device = "cpu",
-                        rope_rows: int = 8192) -> Dict[str, torch.Tensor]:
+                        rope_rows: int = 8192, tiled: Optional[bool] = None) -> Dict[str, torch.Tensor]:
     """Layer-stacked packed weights: w_qkv [L,3072,2048], w_o [L,2048,2048],
     w_gu [L,16384,2048], w_down [L,2048,8192], embed [V,2048], norm_final
-    [2048], rope [rope_rows,128] (cos | sin), all bf16 on ``device``."""
+    [2048], rope [rope_rows,128] (cos | sin), all bf16 on ``device``; with
+    ``tiled`` (default: on a GPU) also t_qkv, t_o, t_gu, t_down, t_embed, the
+    ``mfma_tiles`` copies the batched kernel streams (+2.9 GiB at full size)."""
     L = d.n_layers
     packed = {
         "w_qkv": torch.empty((L, d.qkv_rows, d.hidden), dtype=torch.bfloat16, device=device),
@@ -197,6 +214,11 @@ def pack_for_megakernel(sd: Dict[str, torch.Tensor], d: LlamaDims = LLAMA_3_2_1B
     packed["embed"] = sd["embed_tokens.weight"].to(device).contiguous()
     packed["norm_final"] = sd["norm.weight"].to(device).contiguous()
     packed["rope"] = rope_table(rope_rows, d).to(device)
+    if tiled is None:
+        tiled = torch.device(device).type == "cuda"
+    if tiled:
+        for t, src in (("t_qkv", "w_qkv"), ("t_o", "w_o"), ("t_gu", "w_gu"), ("t_down", "w_down"), ("t_embed", "embed")):
+            packed[t] = mfma_tiles(packed[src])
     return packed
 
 

@@ -119,6 +119,42 @@ def test_batched_layer_matches_oracle(layer1, batch):
     say(f"[blayer] batch={batch}: max ulps (at the operands' scale) {worst_ulps:.2f}, worst rms ratio vs bf16 floor {worst_ratio:.2f}")
 
 
+@pytest.mark.parametrize("batch", [5, 32])
+def test_batched_tiled_weights_bitwise_equal_row_major(layer1, batch):
+    """The MFMA-tiled weight copies only change where each B operand is read
+    from: every MFMA gets the same lane data, so the layer output, the K/V
+    rows, the lm_head logits and the argmax are bit-identical to a run on the
+    row-major stacks (batch 5: one 16-row tile; batch 32: two tiles and the
+    2-D down projection)."""
+    import mk_lib
+    packed = layer1[0]
+    assert all(k in packed for k in mk_lib.TILED_KEYS)
+    pos_list = ragged_positions(batch, S, seed=50 + batch)
+    say(f"[tiled] batch={batch} pos={pos_list}")
+    g = torch.Generator().manual_seed(2000 + batch)
+    hidden = torch.randn(batch, 2048, generator=g).to(torch.bfloat16).cuda()
+    k0 = torch.randn(batch, 8, S, 64, generator=g).to(torch.bfloat16)
+    v0 = torch.randn(batch, 8, S, 64, generator=g).to(torch.bfloat16)
+    runs = []
+    for tiled in (True, False):
+        w = mk_lib.weights_struct(packed, tiled=tiled)
+        assert (w.t_gu is not None) == tiled
+        ws = mk_lib.Workspace(max(batch, 2), S, torch.device("cuda"))
+        kc, vc = k0.cuda(), v0.cuda()
+        pos = torch.tensor(pos_list, dtype=torch.int32, device="cuda")
+        out = torch.empty(batch, 2048, dtype=torch.bfloat16, device="cuda")
+        logits = torch.empty(batch, mk_lib.VOCAB, dtype=torch.float32, device="cuda")
+        nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
+        mk_lib.decode_step(w, ws, [kc], [vc], pos, hidden_in=hidden, hidden_out=out, logits=logits,
+                           next_token=nxt, n_layers=1, batch=batch)
+        torch.cuda.synchronize()
+        assert ws.read_device_error() == 0
+        runs.append((out.cpu().view(torch.int16), kc.cpu().view(torch.int16), vc.cpu().view(torch.int16),
+                     logits.cpu().view(torch.int32), nxt.cpu()))
+    for name, a, b in zip(("hidden", "k", "v", "logits", "next"), *runs):
+        assert torch.equal(a, b), name
+
+
 def test_batched_layer_bad_position_refused(layer1):
     import mk_lib
     packed, _, _ = layer1
