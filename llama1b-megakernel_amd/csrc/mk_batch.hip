@@ -778,7 +778,12 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
   const BParams& p = *c.p;
   const int wave = wave_id(), lane = lane_id();
   int V0, V1, R0, R1;
-  share(VOCAB, c.G, c.w, V0, V1);
+  // vocabulary rows in multiples of 8: in the tiled lm_head the 8 rows of a
+  // lane group are one 128-byte run of each block (a share of 501 rows would
+  // split most 16-row tiles between two workgroups at odd offsets)
+  share(VOCAB / 8, c.G, c.w, V0, V1);
+  V0 *= 8;
+  V1 *= 8;
   share(H, c.G, c.w, R0, R1);
   const int ntile = (V1 - V0 + 15) / 16;
   constexpr int UPT = H / (KS * 32);
