@@ -47,7 +47,8 @@ inline int batch_of_ws_bytes(size_t bytes) {
 //   qkv  bf16 [M][3072]   q | fresh k | fresh v of each token
 //   att  bf16 [M][2048]   merged attention output
 //   h1   bf16 [M][2048]   h + attn
-//   act  bf16 [M][8192]   silu(gate) * up
+//   act  bf16 [M16][8192] silu(gate) * up, M16 = M rounded up to 16, in
+//                         MFMA A-tile order (1 KiB per 16 tokens x 32 columns)
 //   h2   bf16 [M][2048]   layer output
 // and, after all layers, the attention partials
 //   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)]
@@ -64,7 +65,7 @@ struct BatchLayout {
     att = r256(qkv + (size_t)M * MK_QKV_ROWS * 2);
     h1 = r256(att + (size_t)M * MK_HIDDEN * 2);
     act = r256(h1 + (size_t)M * MK_HIDDEN * 2);
-    h2 = r256(act + (size_t)M * MK_INTER * 2);
+    h2 = r256(act + (size_t)((M + 15) / 16 * 16) * MK_INTER * 2);
     layer = r256(h2 + (size_t)M * MK_HIDDEN * 2);
     part_base = (size_t)MK_MAX_LAYERS * layer;
     part_layer = r256((size_t)M * MK_N_KV_HEADS * BATT_MAX_SPLIT * 4 * (MK_HEAD_DIM + 2) * 4);

@@ -245,6 +245,29 @@ __device__ __forceinline__ void load_a(rsrc_t r, int B, int row_elems, int k0, u
   }
 }
 
+// act is exchanged in MFMA A-tile order: for token m and column j, the 1 KiB
+// block (m / 16, j / 32), 16-byte slot ((j % 32) / 8) * 16 + m % 16, element
+// j % 8 (slot = the lane that feeds it to v_mfma_f32_16x16x32_bf16), so each
+// A load of the down projection reads whole 128-byte runs instead of 64 bytes
+// from each token row. Element offset:
+__device__ __forceinline__ size_t act_off(int m, int j) {
+  return ((size_t)(m >> 4) * (INTER / 32) + (size_t)(j >> 5)) * 512 + (size_t)((((j & 31) >> 3) << 4) + (m & 15)) * 8 +
+         (size_t)(j & 7);
+}
+// The A-operand pieces of N k-steps from the tiled act (same register
+// contents as load_a on a row-major [B][INTER] matrix).
+template <int MT, int N>
+__device__ __forceinline__ void load_a_act(rsrc_t r, int B, int k0, u32x4 (&a)[MT * N]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + (lane & 15);
+    const uint32_t o = m < B ? ((uint32_t)(mt * (INTER / 32) + (k0 >> 5)) * 1024u + (uint32_t)lane * 16u) : OOB;
+#pragma unroll
+    for (int s = 0; s < N; ++s) a[mt * N + s] = ld16(r, o + (uint32_t)s * 1024u);
+  }
+}
+
 // Stage the [B][2048] bf16 input of a phase into LDS with buffer loads to LDS
 // (rows >= B zero), then RMS-normalise every row in place, keeping the raw
 // columns [r0, r1) in L.res:
@@ -595,7 +618,7 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
           const float other = dpp<DPP_XOR1>(mine);   // up (row + 1) for a gate lane
           const int m = mt * 16 + (lane >> 4) * 4 + i;
           if (gate && row < row_end && m < c.B)
-            st_dev(act + (size_t)m * INTER + (row >> 1), f2bf(mine / (1.0f + __expf(-mine)) * other));
+            st_dev(act + act_off(m, row >> 1), f2bf(mine / (1.0f + __expf(-mine)) * other));
         }
     }
   };
@@ -620,7 +643,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
   constexpr int UPT = KW / (DKS * 32);    // 8 units per tile
   const int nunits = ntile * UPT;
   const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
-  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)c.B * INTER * 2);
+  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)((c.B + 15) / 16 * 16) * INTER * 2);
   struct Unit {
     u32x4 w[DKS];
     u32x4 a[MT * DKS];
@@ -629,7 +652,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
     load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, wave * KW + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
-    load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, wave * KW + (u % UPT) * DKS * 32, un.a);
+    load_a_act<MT, DKS>(ra, u < nunits ? c.B : 0, wave * KW + (u % UPT) * DKS * 32, un.a);
   };
   Unit ua, ub;
   issue_w(0, ua);
@@ -692,7 +715,7 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
   const int nunits = ntile * UPT;
   const int k0w = kq * (INTER / DN_KQ) + wave * KW;
   const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
-  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)c.B * INTER * 2);
+  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)((c.B + 15) / 16 * 16) * INTER * 2);
   float* dp = c.dpart(li);
   struct Unit {
     u32x4 w[DKS];
@@ -702,7 +725,7 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
     load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, k0w + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
-    load_a<MT, DKS>(ra, u < nunits ? c.B : 0, INTER, k0w + (u % UPT) * DKS * 32, un.a);
+    load_a_act<MT, DKS>(ra, u < nunits ? c.B : 0, k0w + (u % UPT) * DKS * 32, un.a);
   };
   Unit ua, ub;
   issue_w(0, ua);
