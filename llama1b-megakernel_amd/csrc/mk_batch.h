@@ -45,10 +45,10 @@ inline int batch_of_ws_bytes(size_t bytes) {
 // Exchange area of a batched step for up to M sequences (bytes), ordinary
 // device memory. Per layer (each part on a 256-byte boundary):
 //   qkv  bf16 [M][3072]   q | fresh k | fresh v of each token
-//   att  bf16 [M][2048]   merged attention output
+//   att  bf16 [M16][2048] merged attention output, M16 = M rounded up to 16,
+//                         in MFMA A-tile order (1 KiB per 16 tokens x 32 columns)
 //   h1   bf16 [M][2048]   h + attn
-//   act  bf16 [M16][8192] silu(gate) * up, M16 = M rounded up to 16, in
-//                         MFMA A-tile order (1 KiB per 16 tokens x 32 columns)
+//   act  bf16 [M16][8192] silu(gate) * up, in the same order
 //   h2   bf16 [M][2048]   layer output
 // and, after all layers, the attention partials
 //   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)]
@@ -63,7 +63,7 @@ struct BatchLayout {
   void init(int M) {
     qkv = 0;
     att = r256(qkv + (size_t)M * MK_QKV_ROWS * 2);
-    h1 = r256(att + (size_t)M * MK_HIDDEN * 2);
+    h1 = r256(att + (size_t)((M + 15) / 16 * 16) * MK_HIDDEN * 2);
     act = r256(h1 + (size_t)M * MK_HIDDEN * 2);
     h2 = r256(act + (size_t)((M + 15) / 16 * 16) * MK_INTER * 2);
     layer = r256(h2 + (size_t)M * MK_HIDDEN * 2);

@@ -230,39 +230,19 @@ __device__ __forceinline__ void load_w(rsrc_t r, bool tiled, int row, int row_en
   for (int s = 0; s < N; ++s) wv[s] = ld_stream(r, o + (uint32_t)s * step);
 }
 
-// The A-operand pieces of N k-steps read straight from an exchange matrix
-// [B][row_elems] (ordinary loads): a[mt*N + s] = token mt*16 + lane%16,
-// columns k0 + s*32 + (lane/16)*8 .. +7; tokens >= B read zero.
+// att and act are exchanged in MFMA A-tile order (a_tile_off: 1 KiB per 16
+// tokens x 32 columns, the 16 bytes each lane feeds to the MFMA contiguous),
+// so the A loads of the O and down projections read whole 128-byte runs
+// instead of 64 bytes from each token row.
+// The A-operand pieces of N k-steps from such a matrix with kb = columns / 32
+// (lane l: token mt*16 + l%16, columns k0 + s*32 + (l/16)*8 .. +7 for k-step s).
 template <int MT, int N>
-__device__ __forceinline__ void load_a(rsrc_t r, int B, int row_elems, int k0, u32x4 (&a)[MT * N]) {
+__device__ __forceinline__ void load_a_tiled(rsrc_t r, int B, int kb, int k0, u32x4 (&a)[MT * N]) {
   const int lane = lane_id();
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + (lane & 15);
-    const uint32_t o = m < B ? (uint32_t)m * (uint32_t)(row_elems * 2) + (uint32_t)(k0 + (lane >> 4) * 8) * 2u : OOB;
-#pragma unroll
-    for (int s = 0; s < N; ++s) a[mt * N + s] = ld16(r, o + (uint32_t)s * 64u);
-  }
-}
-
-// act is exchanged in MFMA A-tile order: for token m and column j, the 1 KiB
-// block (m / 16, j / 32), 16-byte slot ((j % 32) / 8) * 16 + m % 16, element
-// j % 8 (slot = the lane that feeds it to v_mfma_f32_16x16x32_bf16), so each
-// A load of the down projection reads whole 128-byte runs instead of 64 bytes
-// from each token row. Element offset:
-__device__ __forceinline__ size_t act_off(int m, int j) {
-  return ((size_t)(m >> 4) * (INTER / 32) + (size_t)(j >> 5)) * 512 + (size_t)((((j & 31) >> 3) << 4) + (m & 15)) * 8 +
-         (size_t)(j & 7);
-}
-// The A-operand pieces of N k-steps from the tiled act (same register
-// contents as load_a on a row-major [B][INTER] matrix).
-template <int MT, int N>
-__device__ __forceinline__ void load_a_act(rsrc_t r, int B, int k0, u32x4 (&a)[MT * N]) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + (lane & 15);
-    const uint32_t o = m < B ? ((uint32_t)(mt * (INTER / 32) + (k0 >> 5)) * 1024u + (uint32_t)lane * 16u) : OOB;
+    const uint32_t o = m < B ? ((uint32_t)(mt * kb + (k0 >> 5)) * 1024u + (uint32_t)lane * 16u) : OOB;
 #pragma unroll
     for (int s = 0; s < N; ++s) a[mt * N + s] = ld16(r, o + (uint32_t)s * 1024u);
   }
@@ -520,8 +500,8 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     }
     __syncthreads();
     if (L.flag) {
-      attn_merge_head<false, BATT_MAX_SPLIT>(c.s, c.part(li, b, h, 0), nsb,
-                                             c.xb(li, p.lay.att) + (size_t)b * H + h * GQA * HD);
+      attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, c.part(li, b, h, 0), nsb, c.xb(li, p.lay.att), b,
+                                                   h * GQA * HD);
       arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
     }
   }
@@ -544,7 +524,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
   wait_handover(c.s, c.ho(li, HO_ATT), c.B, 0);
   trace_mark(c.s, 2 * xk(li, 3));
   u32x4 a[MT * KS];
-  load_a<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)c.B * H * 2), c.B, H, wave * KQ, a);
+  load_a_tiled<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)((c.B + 15) / 16 * 16) * H * 2), c.B, H / 32, wave * KQ, a);
   uint16_t* h1 = c.xb(li, p.lay.h1);
   for (int tt = 0; tt < ntile; ++tt) {
     f32x4 acc[MT];
@@ -618,7 +598,7 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
           const float other = dpp<DPP_XOR1>(mine);   // up (row + 1) for a gate lane
           const int m = mt * 16 + (lane >> 4) * 4 + i;
           if (gate && row < row_end && m < c.B)
-            st_dev(act + act_off(m, row >> 1), f2bf(mine / (1.0f + __expf(-mine)) * other));
+            st_dev(act + a_tile_off(m, row >> 1, INTER / 32), f2bf(mine / (1.0f + __expf(-mine)) * other));
         }
     }
   };
@@ -652,7 +632,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
     load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, wave * KW + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
-    load_a_act<MT, DKS>(ra, u < nunits ? c.B : 0, wave * KW + (u % UPT) * DKS * 32, un.a);
+    load_a_tiled<MT, DKS>(ra, u < nunits ? c.B : 0, INTER / 32, wave * KW + (u % UPT) * DKS * 32, un.a);
   };
   Unit ua, ub;
   issue_w(0, ua);
@@ -725,7 +705,7 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
     load_w<DKS>(rw, p.tiled, u < nunits ? R0 + 16 * (u / UPT) : R1, R1, INTER * 2, k0w + (u % UPT) * DKS * 32, un.w);
   };
   auto issue_a = [&](int u, Unit& un) {
-    load_a_act<MT, DKS>(ra, u < nunits ? c.B : 0, k0w + (u % UPT) * DKS * 32, un.a);
+    load_a_tiled<MT, DKS>(ra, u < nunits ? c.B : 0, INTER / 32, k0w + (u % UPT) * DKS * 32, un.a);
   };
   Unit ua, ub;
   issue_w(0, ua);

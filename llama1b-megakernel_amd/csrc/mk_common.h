@@ -754,8 +754,22 @@ __device__ __forceinline__ void attn_split(int n_rows, int max_split, int min_ro
 // the caller knows they are complete and they are read once (device scope).
 // MAXS: the most splits a call may pass.
 constexpr int ATT_MERGE_MAX = 8;   // splits the polled merge reads at most
-template <bool POLL = true, int MAXS = ATT_MERGE_MAX>
-__device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* part_head, int nsplit, uint16_t* att) {
+
+// Element offset of (row m, column j) in a bf16 matrix kept in MFMA A-tile
+// order with kblocks = columns / 32: the 1 KiB block (m / 16, j / 32), 16-byte
+// slot ((j % 32) / 8) * 16 + m % 16 (the lane of v_mfma_f32_16x16x32_bf16 that
+// takes it), element j % 8.
+__device__ __forceinline__ size_t a_tile_off(int m, int j, int kblocks) {
+  return ((size_t)(m >> 4) * (size_t)kblocks + (size_t)(j >> 5)) * 512 +
+         (size_t)((((j & 31) >> 3) << 4) + (m & 15)) * 8 + (size_t)(j & 7);
+}
+
+// TILED: att is the base of a [tokens][2048] matrix in A-tile order and the
+// head's 256 outputs go to row tok, columns col0 ..; otherwise att points at
+// the head's 256 contiguous outputs.
+template <bool POLL = true, int MAXS = ATT_MERGE_MAX, bool TILED = false>
+__device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* part_head, int nsplit, uint16_t* att,
+                                                int tok = 0, int col0 = 0) {
   const int t = threadIdx.x, g = t >> 6, d = t & 63;
   const rsrc_t r = make_rsrc(part_head, (size_t)nsplit * PART_FLOATS * 4);
   uint32_t m[MAXS], l[MAXS], o[MAXS];
@@ -789,7 +803,10 @@ __device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* par
   }
   const uint32_t mine = f2bf(O / Lsum);
   const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine, DPP_XOR1, 0xf, 0xf, false);
-  if ((d & 1) == 0) st_dev(reinterpret_cast<uint32_t*>(att + g * HD + d), mine | (next << 16));
+  if ((d & 1) == 0) {
+    uint16_t* dst = TILED ? att + a_tile_off(tok, col0 + g * HD + d, 2048 / 32) : att + g * HD + d;
+    st_dev(reinterpret_cast<uint32_t*>(dst), mine | (next << 16));
+  }
 }
 
 }  // namespace mk
