@@ -65,6 +65,40 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def timed_steps(launch, K: int):
+    """Time K back-to-back launches with HIP events only around the whole
+    run (an event recorded between two launches puts a marker packet between
+    the kernels, which costs several us per step on this stack), bracketed by
+    synchronisations; returns (host wall s, mean ms per step from the events)."""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    e0.record()
+    for _ in range(K):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    return wall, e0.elapsed_time(e1) / K
+
+
+def step_latencies(launch, K: int, reset):
+    """After the timed run: reset the state and run the same K steps again
+    with an event after each, for the per-step latency percentiles (each
+    interval includes its event marker)."""
+    import torch
+    reset()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i in range(K):
+        launch()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
+
+
 def cpu_baseline(sd, n_steps: int, budget_s: float):
     """The oracle's decode step (fp32 accumulation, bf16 rounding points) on the
     host cores, at positions 384.. with a synthetic N(0,1) KV cache."""
@@ -169,20 +203,17 @@ def main():
     torch.cuda.synchronize()
 
     K = args.steps
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    evs[0].record()
-    for i in range(K):
-        dec.launch()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
+
+    def reset():
+        model.pos.copy_(pos0)
+        model.tokens.copy_(tok0)
+        torch.cuda.synchronize()
+
+    wall, mean_ms = timed_steps(dec.launch, K)
+    step_ms = step_latencies(dec.launch, K, reset)
     bits = model.ws.read_device_error()
     if bits:
         sys.exit(f"device error bits 0x{bits:x}")
-    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
-    mean_ms = sum(step_ms) / K
     bytes_per_step = sum(step_bytes(16, [PROMPT + i], lm_head=True) for i in range(K)) / K
     achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
 
@@ -247,20 +278,12 @@ def run_layer(args):
         step.launch()          # every launch recomputes the same layer (row POS rewritten identically)
     torch.cuda.synchronize()
     K = args.steps
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    evs[0].record()
-    for i in range(K):
-        step.launch()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
+    wall, mean_ms = timed_steps(step.launch, K)
+    us = [v * 1e3 for v in step_latencies(step.launch, K, lambda: None)]
     bits = ws.read_device_error()
     if bits:
         sys.exit(f"device error bits 0x{bits:x}")
-    us = [evs[i].elapsed_time(evs[i + 1]) * 1e3 for i in range(K)]
-    mean_us = sum(us) / K
+    mean_us = mean_ms * 1e3
     nbytes = step_bytes(1, [POS], lm_head=False) + 2048 * 2   # + the hidden_out row
     achieved = nbytes / (mean_us * 1e-6) / 1e9
     result = {
@@ -341,20 +364,17 @@ def run_batched(args, cfg):
     torch.cuda.synchronize()
     pos.copy_(pos0)
     toks.copy_(tok0)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    evs[0].record()
-    for i in range(K):
-        step.launch()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
+
+    def reset():
+        pos.copy_(pos0)
+        toks.copy_(tok0)
+        torch.cuda.synchronize()
+
+    wall, mean_ms = timed_steps(step.launch, K)
+    step_ms = step_latencies(step.launch, K, reset)
     bits = ws.read_device_error()
     if bits:
         sys.exit(f"device error bits 0x{bits:x}")
-    step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
-    mean_ms = sum(step_ms) / K
     bytes_per_step = sum(step_bytes(16, [p + i for p in starts], lm_head=True) for i in range(K)) / K
     achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
     result = {
