@@ -1,4 +1,4 @@
-"""The HF checkpoint path (SURVEY §8(f) 4): ``mk_weights.load_hf_checkpoint``
+"""The HF checkpoint path: ``mk_weights.load_hf_checkpoint``
 reads a local safetensors checkpoint into the naming the packer consumes, the
 input format on the far side of the reference's convert_hf_to_neuron_state_dict
 (llama_with_megakernel.py:281-351; tied lm_head, llama.py:1404-1406).
