@@ -229,8 +229,28 @@ long long mk_wall_clock_hz(int device);
 
 /* Workspace bytes for `batch` sequences with `s_max` cache rows; 0 if unsupported. */
 size_t mk_workspace_bytes(int32_t batch, int32_t s_max);
-/* Initialise the workspace on `stream` with a fill kernel (graph-capturable). */
+/*
+ * Initialise the workspace on `stream` with fill kernels. The first call for
+ * a workspace address on a device also ALLOCATES its exchange area (the
+ * per-layer hand-over buffers the kernel's workgroups pass results through):
+ * 3.2 MB of uncached device memory for a batch-1 workspace, or
+ * BatchLayout(batch) bytes (about 100 MB at batch 32) of ordinary device
+ * memory for a batched one. So this call must not be made under stream
+ * capture; later calls for the same workspace only launch the fills. At most
+ * 256 exchange areas exist at once per process (MK_ERR_WORKSPACE beyond).
+ * No counterpart in the reference (its NKI kernel keeps its state on chip).
+ */
 int mk_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+/*
+ * Return the exchange area of a workspace initialised on the current device:
+ * synchronises the device (every step that used it has finished), then frees
+ * a batched area, or keeps a batch-1 (uncached) area as a spare that the next
+ * mk_workspace_init reuses (uncached memory a kernel has read is never freed
+ * while the process runs). The workspace must be initialised again before its
+ * next step. Lifecycle counterpart of mk_workspace_init; no counterpart in
+ * the reference.
+ */
+int mk_workspace_release(void *workspace);
 /* Synchronise `stream`, return the device error bits and clear them. */
 int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);
 

@@ -892,7 +892,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 //     through its XCD's L2.
 // A workspace re-initialised with another layout (a new allocation at the
 // same address) gets a matching area; areas it no longer uses stay in the
-// list and are handed to the next workspace that fits.
+// list and are handed to the next workspace that fits. mk_workspace_release
+// returns a workspace's area: an uncached one becomes spare (never freed), an
+// ordinary one is freed and its entry removed.
 constexpr size_t XCH_BYTES = 2 * SET_BYTES;
 struct XchEntry {
   const void* ws;   // owner (nullptr: spare)
@@ -955,6 +957,25 @@ int exchange_create(const void* ws, int dev, int max_batch, XchEntry* out) {
   return MK_OK;
 }
 
+// Release the exchange area owned by `ws` on `dev` (see above). The caller
+// has synchronised the device, so no kernel still uses the area.
+int exchange_release(const void* ws, int dev) {
+  std::lock_guard<std::mutex> lk(g_xch_mu);
+  for (int i = 0; i < g_n_xch; ++i) {
+    XchEntry& e = g_xch[i];
+    if (e.ws != ws || e.dev != dev) continue;
+    if (e.max_batch == 1) {   // uncached: read by kernels, so kept until the process ends
+      e.ws = nullptr;
+      return MK_OK;
+    }
+    const hipError_t he = hipFree(e.xch);
+    g_xch[i] = g_xch[--g_n_xch];
+    if (he != hipSuccess) return fail(MK_ERR_HIP, "freeing the exchange area: %s", hipGetErrorString(he));
+    return MK_OK;
+  }
+  return fail(MK_ERR_WORKSPACE, "workspace %p has no exchange area on device %d", ws, dev);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1001,6 +1022,16 @@ int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MK_ERR_HIP, "workspace init launch: %s", hipGetErrorString(e));
   return MK_OK;
+}
+
+int mk_workspace_release(void* workspace) {
+  if (!workspace) return fail(MK_ERR_NULL, "workspace is NULL");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
+  // every kernel that may still use the workspace's exchange area has finished
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "hipDeviceSynchronize: %s", hipGetErrorString(e));
+  return exchange_release(workspace, dev);
 }
 
 int mk_read_device_error(void* workspace, void* stream, uint32_t* bits_out) {

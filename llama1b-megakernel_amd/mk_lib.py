@@ -94,6 +94,8 @@ def load() -> ctypes.CDLL:
         lib.mk_workspace_bytes.restype = c_size_t
         lib.mk_workspace_init.argtypes = [c_void_p, c_size_t, c_void_p]
         lib.mk_workspace_init.restype = c_int
+        lib.mk_workspace_release.argtypes = [c_void_p]
+        lib.mk_workspace_release.restype = c_int
         lib.mk_read_device_error.argtypes = [c_void_p, c_void_p, POINTER(c_uint32)]
         lib.mk_read_device_error.restype = c_int
         lib.mk_decode_step.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
@@ -144,7 +146,9 @@ def weights_struct(packed: Dict[str, torch.Tensor], tiled: bool = True) -> MkWei
 
 
 class Workspace:
-    """Device workspace for one stream of steps (zeroed once at creation)."""
+    """Device workspace for one stream of steps (initialised once at creation;
+    the library's exchange area for it is returned by ``release()``, which
+    also runs when the object is garbage-collected)."""
 
     def __init__(self, batch: int, s_max: int, device: torch.device):
         lib = load()
@@ -152,10 +156,29 @@ class Workspace:
         if n == 0:
             raise MkError(-4, f"no workspace size for batch={batch}, s_max={s_max}")
         self.nbytes = (n + 255) // 256 * 256
+        self.device = torch.device(device)
         # torch's caching allocator returns 512-byte aligned blocks
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
         assert self.buf.data_ptr() % 256 == 0
+        self._live = False
         check(lib.mk_workspace_init(self.buf.data_ptr(), self.nbytes, c_void_p(current_stream_ptr())))
+        self._live = True
+
+    def release(self) -> None:
+        """mk_workspace_release: synchronises the device and returns the
+        exchange area (the workspace is unusable afterwards)."""
+        if self._live:
+            self._live = False
+            with torch.cuda.device(self.device):
+                check(load().mk_workspace_release(self.buf.data_ptr()))
+
+    def __del__(self):
+        import sys
+        if getattr(self, "_live", False) and not sys.is_finalizing():
+            try:
+                self.release()
+            except Exception:   # never raise from a finaliser
+                pass
 
     def read_device_error(self) -> int:
         bits = c_uint32(0)

@@ -111,3 +111,8 @@ def test_layer_step_requires_hidden(lib):
     rc = lib.mk_layer_step(ctypes.byref(w), 0, 1, 1024, 0x1000, 0x2000, None, 0x4000, 0x5000, 0x100000,
                            1 << 24, None)
     assert rc == -1
+
+
+def test_workspace_release_requires_workspace(lib):
+    assert lib.mk_workspace_release(None) == -1
+    assert b"NULL" in lib.mk_last_error()
