@@ -258,6 +258,32 @@ int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);
 int mk_decode_step(const mk_weights *w, const mk_step_args *a);
 
 /*
+ * Allocation-free variant of mk_decode_step. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc), so it takes
+ * no workspace and needs no mk_workspace_init.
+ *   The kernel's scratch (the control block and both sets of per-layer
+ *   exchange buffers of the batch-1 kernel) is a static device array inside
+ *   the library, MK_NOALLOC_SCRATCH_BYTES per device, held until the process
+ *   ends. The library looks its address up on its first call on a device and
+ *   fills it there (a fill kernel on `stream`; repeated on the next call if
+ *   that first call was under stream capture). Nothing is allocated or freed.
+ *   Same arguments and results as mk_decode_step, except:
+ *     - batch must be 1 (MK_ERR_SHAPE otherwise) and MK_FLAG_PREFILL is
+ *       refused (MK_ERR_UNSUPPORTED): the scratch holds batch-1 buffers only;
+ *     - workspace must be NULL and workspace_bytes 0 (MK_ERR_WORKSPACE);
+ *     - device-detected faults (MK_DEVERR_*) are not kept for
+ *       mk_read_device_error: a faulted step writes next_token[0] = -1 (if
+ *       next_token is given) and does not advance pos.
+ *   Every call of this entry point on one device shares that device's
+ *   scratch, and each call leaves it ready for the next: calls that overlap
+ *   in time on one device (e.g. on two unordered streams) race and give
+ *   wrong results. Order them (one stream, or events).
+ */
+#define MK_NOALLOC_SCRATCH_BYTES 3277056
+int mk_decode_step_noalloc(const mk_weights *w, const mk_step_args *a);
+
+/*
  * Single-layer step (transformer_llama_megakernel_1layer,
  * transformer_llama.py:154-191): layer `layer` of the stacks applied to
  * hidden_in, result in hidden_out, K/V row pos[b] written in place.

@@ -161,6 +161,7 @@ struct KParams {
   int s_max;
   int rope_rows;
   int do_lm;
+  int noalloc;   // control block and exchange sets in the library's static scratch
   uint32_t flags;
   unsigned long long timeout_ticks;
   unsigned long long* trace;
@@ -813,13 +814,25 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   if (!L.last || threadIdx.x != 0) return;
   ctrl[C_EXIT] = 0u;
   ctrl[C_EPOCH] = epoch + 1u;
-  if (pos_ok) {
-    if (p.do_lm) {
-      unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + C_KEY_BYTE);
-      const unsigned long long key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *kp = 0ull;
-      if (p.next_token) p.next_token[0] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+  unsigned long long key = 0ull;
+  if (pos_ok && p.do_lm) {
+    unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + C_KEY_BYTE);
+    key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *kp = 0ull;
+  }
+  if (p.noalloc) {
+    // The static scratch has no reader for error bits: a faulted step reports
+    // next_token = -1 (and does not advance), and the bits are cleared so the
+    // next step's waits do not bail out.
+    const uint32_t bits = __hip_atomic_load(ctrl + C_ERR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ctrl[C_ERR] = 0u;
+    if (bits) {
+      if (p.next_token) p.next_token[0] = -1;
+      return;
     }
+  }
+  if (pos_ok) {
+    if (p.do_lm && p.next_token) p.next_token[0] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
     if (p.flags & MK_FLAG_ADVANCE) p.pos[0] = c.pos + 1;
   }
 }
@@ -976,6 +989,135 @@ int exchange_release(const void* ws, int dev) {
   return fail(MK_ERR_WORKSPACE, "workspace %p has no exchange area on device %d", ws, dev);
 }
 
+
+// Argument checks shared by mk_decode_step and mk_decode_step_noalloc (all but the workspace).
+int check_step_args(const mk_weights* w, const mk_step_args* a) {
+  if (!w || !a) return fail(MK_ERR_NULL, "weights or args is NULL");
+  if (a->n_layers < 1 || a->first_layer < 0 || a->first_layer + a->n_layers > w->n_layers ||
+      w->n_layers > MK_MAX_LAYERS)
+    return fail(MK_ERR_SHAPE, "layers [%d, %d) not within the %d packed layers (max %d)", a->first_layer,
+                a->first_layer + a->n_layers, w->n_layers, MK_MAX_LAYERS);
+  if (a->batch < 1) return fail(MK_ERR_SHAPE, "batch %d < 1", a->batch);
+  if (a->batch > BATCH_MAX) return fail(MK_ERR_SHAPE, "batch %d > %d", a->batch, BATCH_MAX);
+  if (a->s_max < 1 || a->s_max > w->rope_rows)
+    return fail(MK_ERR_SHAPE, "s_max %d must be in [1, rope_rows=%d]", a->s_max, w->rope_rows);
+  if (!a->k_cache || !a->v_cache) return fail(MK_ERR_NULL, "k_cache / v_cache array is NULL");
+  for (int i = 0; i < a->n_layers; ++i) {
+    if (!a->k_cache[i] || !a->v_cache[i]) return fail(MK_ERR_NULL, "cache pointer of layer %d is NULL", i);
+    if (!aligned16(a->k_cache[i]) || !aligned16(a->v_cache[i]))
+      return fail(MK_ERR_ALIGN, "cache of layer %d is not 16-byte aligned", i);
+  }
+  if ((a->tokens == nullptr) == (a->hidden_in == nullptr))
+    return fail(MK_ERR_NULL, "exactly one of tokens / hidden_in must be given");
+  if (!a->pos) return fail(MK_ERR_NULL, "pos is NULL");
+  const bool do_lm = a->logits != nullptr || a->next_token != nullptr;
+  if (!w->w_qkv || !w->w_o || !w->w_gu || !w->w_down || !w->rope)
+    return fail(MK_ERR_NULL, "a layer weight pointer is NULL");
+  if ((do_lm || a->tokens) && !w->embed) return fail(MK_ERR_NULL, "embed is NULL");
+  if (do_lm && !w->norm_final) return fail(MK_ERR_NULL, "norm_final is NULL");
+  const void* al[] = {w->w_qkv, w->w_o, w->w_gu, w->w_down, w->embed, w->norm_final, a->hidden_in, a->hidden_out};
+  for (const void* q : al)
+    if (q && !aligned16(q)) return fail(MK_ERR_ALIGN, "a weight or hidden pointer is not 16-byte aligned");
+  return MK_OK;
+}
+
+// Enqueue mk_decode_kernel (batch 1) with control block `ctrl` and exchange sets `xch`.
+int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& di, uint8_t* ctrl, uint8_t* xch,
+                  bool noalloc) {
+  const bool do_lm = a->logits != nullptr || a->next_token != nullptr;
+  KParams kp;
+  memset(&kp, 0, sizeof(kp));
+  kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
+  kp.w_o = static_cast<const uint16_t*>(w->w_o);
+  kp.w_gu = static_cast<const uint16_t*>(w->w_gu);
+  kp.w_d = static_cast<const uint16_t*>(w->w_down);
+  kp.embed = static_cast<const uint16_t*>(w->embed);
+  kp.g_final = static_cast<const uint16_t*>(w->norm_final);
+  kp.rope = static_cast<const uint16_t*>(w->rope);
+  for (int i = 0; i < a->n_layers; ++i) {
+    kp.kc[i] = static_cast<uint16_t*>(a->k_cache[i]);
+    kp.vc[i] = static_cast<uint16_t*>(a->v_cache[i]);
+  }
+  kp.tokens = a->tokens;
+  kp.hidden_in = static_cast<const uint16_t*>(a->hidden_in);
+  kp.pos = a->pos;
+  kp.hidden_out = static_cast<uint16_t*>(a->hidden_out);
+  kp.logits = a->logits;
+  kp.next_token = a->next_token;
+  kp.ws = ctrl;
+  kp.xch = xch;
+  kp.first_layer = a->first_layer;
+  kp.n_layers = a->n_layers;
+  kp.s_max = a->s_max;
+  kp.rope_rows = w->rope_rows;
+  kp.do_lm = do_lm ? 1 : 0;
+  kp.noalloc = noalloc ? 1 : 0;
+  kp.flags = a->flags;
+  kp.timeout_ticks = di.ticks_per_s * 2ull;   // 2 s per hand-over wait
+  kp.trace = static_cast<unsigned long long*>(a->trace);
+
+  void* args[] = {&kp};
+  // One workgroup per CU with occupancy 1 (checked in device_info): on an
+  // otherwise idle device a plain launch makes every workgroup resident at
+  // once, and leaves ~20 us less between consecutive steps than a cooperative
+  // launch. MK_FLAG_COOPERATIVE asks for the guarantee. Every wait in the
+  // kernel is bounded, so a workgroup that is never scheduled shows up as
+  // MK_DEVERR_SYNC, not as a hang.
+  const hipStream_t st = static_cast<hipStream_t>(a->stream);
+  const hipError_t e =
+      (a->flags & MK_FLAG_COOPERATIVE)
+          ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args,
+                                       0, st)
+          : hipLaunchKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args, 0, st);
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return MK_OK;
+}
+
+// Scratch of mk_decode_step_noalloc, for callers that cannot allocate: the
+// batch-1 control block followed by both exchange sets, in ordinary device
+// memory (each device that runs the library holds its own copy until the
+// process ends). Host code never uses the array's name as an address (on the
+// host it is only a stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, once per device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = CTRL_BYTES + XCH_BYTES;   // 3,277,056 bytes
+static_assert(NOALLOC_SCRATCH_BYTES == 3277056, "scratch size stated in mk.h");
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+struct NoAllocDev {
+  uint8_t* ptr;    // device address of `scratch` on this device
+  bool filled;     // its initial fill has run outside stream capture
+};
+NoAllocDev g_noalloc[64];
+std::mutex g_noalloc_mu;
+
+// The device's scratch address (looked up on its first use there, with the
+// device current); until a fill has run outside stream capture, a fill kernel
+// (control block zero, exchange sets the sentinel) is enqueued first on `st`.
+int noalloc_scratch(int dev, hipStream_t st, uint8_t** out) {
+  if (dev < 0 || dev >= 64) return fail(MK_ERR_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  NoAllocDev& d = g_noalloc[dev];
+  if (!d.ptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(MK_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    d.ptr = static_cast<uint8_t*>(ptr);
+  }
+  if (!d.filled) {
+    hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(d.ptr),
+                       NOALLOC_SCRATCH_BYTES / 16, CTRL_BYTES / 16);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(MK_ERR_HIP, "scratch fill launch: %s", hipGetErrorString(e));
+    // A fill recorded into a graph under capture has not run yet: fill again
+    // on the next call outside capture.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusActive;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) d.filled = true;
+  }
+  *out = d.ptr;
+  return MK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1049,32 +1191,8 @@ int mk_read_device_error(void* workspace, void* stream, uint32_t* bits_out) {
 }
 
 int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
-  if (!w || !a) return fail(MK_ERR_NULL, "weights or args is NULL");
-  if (a->n_layers < 1 || a->first_layer < 0 || a->first_layer + a->n_layers > w->n_layers ||
-      w->n_layers > MK_MAX_LAYERS)
-    return fail(MK_ERR_SHAPE, "layers [%d, %d) not within the %d packed layers (max %d)", a->first_layer,
-                a->first_layer + a->n_layers, w->n_layers, MK_MAX_LAYERS);
-  if (a->batch < 1) return fail(MK_ERR_SHAPE, "batch %d < 1", a->batch);
-  if (a->batch > BATCH_MAX) return fail(MK_ERR_SHAPE, "batch %d > %d", a->batch, BATCH_MAX);
-  if (a->s_max < 1 || a->s_max > w->rope_rows)
-    return fail(MK_ERR_SHAPE, "s_max %d must be in [1, rope_rows=%d]", a->s_max, w->rope_rows);
-  if (!a->k_cache || !a->v_cache) return fail(MK_ERR_NULL, "k_cache / v_cache array is NULL");
-  for (int i = 0; i < a->n_layers; ++i) {
-    if (!a->k_cache[i] || !a->v_cache[i]) return fail(MK_ERR_NULL, "cache pointer of layer %d is NULL", i);
-    if (!aligned16(a->k_cache[i]) || !aligned16(a->v_cache[i]))
-      return fail(MK_ERR_ALIGN, "cache of layer %d is not 16-byte aligned", i);
-  }
-  if ((a->tokens == nullptr) == (a->hidden_in == nullptr))
-    return fail(MK_ERR_NULL, "exactly one of tokens / hidden_in must be given");
-  if (!a->pos) return fail(MK_ERR_NULL, "pos is NULL");
-  const bool do_lm = a->logits != nullptr || a->next_token != nullptr;
-  if (!w->w_qkv || !w->w_o || !w->w_gu || !w->w_down || !w->rope)
-    return fail(MK_ERR_NULL, "a layer weight pointer is NULL");
-  if ((do_lm || a->tokens) && !w->embed) return fail(MK_ERR_NULL, "embed is NULL");
-  if (do_lm && !w->norm_final) return fail(MK_ERR_NULL, "norm_final is NULL");
-  const void* al[] = {w->w_qkv, w->w_o, w->w_gu, w->w_down, w->embed, w->norm_final, a->hidden_in, a->hidden_out};
-  for (const void* q : al)
-    if (q && !aligned16(q)) return fail(MK_ERR_ALIGN, "a weight or hidden pointer is not 16-byte aligned");
+  int rc = check_step_args(w, a);
+  if (rc != MK_OK) return rc;
   if (!a->workspace) return fail(MK_ERR_NULL, "workspace is NULL");
   if (reinterpret_cast<uintptr_t>(a->workspace) & 255u) return fail(MK_ERR_WORKSPACE, "workspace not 256-byte aligned");
   const size_t need = mk_workspace_bytes(a->batch, a->s_max);
@@ -1084,7 +1202,7 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
   DeviceInfo di;
-  const int rc = device_info(dev, &di);
+  rc = device_info(dev, &di);
   if (rc != MK_OK) return rc;
   XchEntry xe;
   if (!exchange_of(a->workspace, dev, &xe))
@@ -1105,53 +1223,28 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
     if (be != hipSuccess) return fail(MK_ERR_HIP, "batched kernel launch failed: %s", hipGetErrorString(be));
     return MK_OK;
   }
-  uint8_t* xch = xe.xch;
+  return launch_decode(w, a, di, static_cast<uint8_t*>(a->workspace), xe.xch, false);
+}
 
-  KParams kp;
-  memset(&kp, 0, sizeof(kp));
-  kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
-  kp.w_o = static_cast<const uint16_t*>(w->w_o);
-  kp.w_gu = static_cast<const uint16_t*>(w->w_gu);
-  kp.w_d = static_cast<const uint16_t*>(w->w_down);
-  kp.embed = static_cast<const uint16_t*>(w->embed);
-  kp.g_final = static_cast<const uint16_t*>(w->norm_final);
-  kp.rope = static_cast<const uint16_t*>(w->rope);
-  for (int i = 0; i < a->n_layers; ++i) {
-    kp.kc[i] = static_cast<uint16_t*>(a->k_cache[i]);
-    kp.vc[i] = static_cast<uint16_t*>(a->v_cache[i]);
-  }
-  kp.tokens = a->tokens;
-  kp.hidden_in = static_cast<const uint16_t*>(a->hidden_in);
-  kp.pos = a->pos;
-  kp.hidden_out = static_cast<uint16_t*>(a->hidden_out);
-  kp.logits = a->logits;
-  kp.next_token = a->next_token;
-  kp.ws = static_cast<uint8_t*>(a->workspace);
-  kp.xch = xch;
-  kp.first_layer = a->first_layer;
-  kp.n_layers = a->n_layers;
-  kp.s_max = a->s_max;
-  kp.rope_rows = w->rope_rows;
-  kp.do_lm = do_lm ? 1 : 0;
-  kp.flags = a->flags;
-  kp.timeout_ticks = di.ticks_per_s * 2ull;   // 2 s per hand-over wait
-  kp.trace = static_cast<unsigned long long*>(a->trace);
-
-  void* args[] = {&kp};
-  // One workgroup per CU with occupancy 1 (checked in device_info): on an
-  // otherwise idle device a plain launch makes every workgroup resident at
-  // once, and leaves ~20 us less between consecutive steps than a cooperative
-  // launch. MK_FLAG_COOPERATIVE asks for the guarantee. Every wait in the
-  // kernel is bounded, so a workgroup that is never scheduled shows up as
-  // MK_DEVERR_SYNC, not as a hang.
-  const hipStream_t st = static_cast<hipStream_t>(a->stream);
-  const hipError_t e =
-      (a->flags & MK_FLAG_COOPERATIVE)
-          ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args,
-                                       0, st)
-          : hipLaunchKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args, 0, st);
-  if (e != hipSuccess) return fail(MK_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return MK_OK;
+int mk_decode_step_noalloc(const mk_weights* w, const mk_step_args* a) {
+  int rc = check_step_args(w, a);
+  if (rc != MK_OK) return rc;
+  if (a->batch != 1)
+    return fail(MK_ERR_SHAPE, "batch %d: the allocation-free step serves batch 1 (its %zu-byte scratch holds the "
+                "batch-1 exchange sets)", a->batch, NOALLOC_SCRATCH_BYTES);
+  if (a->flags & MK_FLAG_PREFILL)
+    return fail(MK_ERR_UNSUPPORTED, "MK_FLAG_PREFILL needs the batched kernel; the allocation-free step is batch 1");
+  if (a->workspace || a->workspace_bytes)
+    return fail(MK_ERR_WORKSPACE, "the allocation-free step takes no workspace (it uses the library's scratch)");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
+  DeviceInfo di;
+  rc = device_info(dev, &di);
+  if (rc != MK_OK) return rc;
+  uint8_t* base = nullptr;
+  rc = noalloc_scratch(dev, static_cast<hipStream_t>(a->stream), &base);
+  if (rc != MK_OK) return rc;
+  return launch_decode(w, a, di, base, base + CTRL_BYTES, true);
 }
 
 int mk_layer_step(const mk_weights* w, int32_t layer, int32_t batch, int32_t s_max, void* k_cache, void* v_cache,

@@ -9,6 +9,7 @@ fallback implementation of the decode step.
 from __future__ import annotations
 
 import ctypes
+import sys
 from ctypes import POINTER, c_char_p, c_int, c_int32, c_size_t, c_uint32, c_void_p
 from pathlib import Path
 from typing import Dict, List, Optional, Sequence
@@ -100,6 +101,8 @@ def load() -> ctypes.CDLL:
         lib.mk_read_device_error.restype = c_int
         lib.mk_decode_step.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
         lib.mk_decode_step.restype = c_int
+        lib.mk_decode_step_noalloc.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
+        lib.mk_decode_step_noalloc.restype = c_int
         lib.mk_layer_step.argtypes = [POINTER(MkWeights), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.mk_layer_step.restype = c_int
@@ -173,7 +176,6 @@ class Workspace:
                 check(load().mk_workspace_release(self.buf.data_ptr()))
 
     def __del__(self):
-        import sys
         if getattr(self, "_live", False) and not sys.is_finalizing():
             try:
                 self.release()
@@ -206,6 +208,24 @@ def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tens
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes,
                    current_stream_ptr(), _ptr(trace))
     check(load().mk_decode_step(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def decode_step_noalloc(weights: MkWeights, k_caches: Sequence[torch.Tensor], v_caches: Sequence[torch.Tensor],
+                        pos: torch.Tensor, *, tokens: Optional[torch.Tensor] = None,
+                        hidden_in: Optional[torch.Tensor] = None, hidden_out: Optional[torch.Tensor] = None,
+                        logits: Optional[torch.Tensor] = None, next_token: Optional[torch.Tensor] = None,
+                        first_layer: int = 0, n_layers: Optional[int] = None, flags: int = 0) -> None:
+    """One call of ``mk_decode_step_noalloc`` (batch 1, no workspace: the
+    library's static scratch) on the current torch stream."""
+    n = len(k_caches) if n_layers is None else n_layers
+    if len(k_caches) < n or len(v_caches) < n:
+        raise ValueError("need one K and one V cache per layer run")
+    kc = (c_void_p * n)(*[t.data_ptr() for t in k_caches[:n]])
+    vc = (c_void_p * n)(*[t.data_ptr() for t in v_caches[:n]])
+    a = MkStepArgs(first_layer, n, 1, int(k_caches[0].shape[-2]), ctypes.cast(kc, POINTER(c_void_p)),
+                   ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
+                   _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, None, 0, current_stream_ptr(), None)
+    check(load().mk_decode_step_noalloc(ctypes.byref(weights), ctypes.byref(a)))
 
 
 def prepare_sampling_params(batch_size: int, top_k, top_p, temperature, device="cuda") -> torch.Tensor:

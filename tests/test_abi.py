@@ -116,3 +116,17 @@ def test_layer_step_requires_hidden(lib):
 def test_workspace_release_requires_workspace(lib):
     assert lib.mk_workspace_release(None) == -1
     assert b"NULL" in lib.mk_last_error()
+
+
+def test_noalloc_step_argument_checks(lib):
+    """mk_decode_step_noalloc: batch 1 only, no prefill, no workspace (checked before any HIP call)."""
+    w = _weights()
+    a, keep = _args(workspace=None, workspace_bytes=0, batch=2)
+    assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -2
+    assert b"batch 1" in lib.mk_last_error()
+    a, keep = _args(workspace=None, workspace_bytes=0, flags=4)
+    assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -4
+    a, keep = _args()
+    assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -3
+    a, keep = _args(workspace=None, workspace_bytes=0, pos=None)
+    assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -1
