@@ -47,3 +47,20 @@ def new_caches(n_layers, s_max, device="cuda", fill=None, seed=0):
         ks.append(k.to(device))
         vs.append(v.to(device))
     return ks, vs
+
+
+def record_parity(name: str, data: dict) -> None:
+    """Write a test's measured parity numbers to gpurun_out/parity/<name>.json
+    (the directory comes back from a GPU run; profiles/parity_summary.md
+    cites these files)."""
+    import json
+    import os
+    from pathlib import Path
+    out = Path(os.environ.get("MK_PARITY_DIR", Path(__file__).resolve().parents[1] / "gpurun_out" / "parity"))
+    out.mkdir(parents=True, exist_ok=True)
+    (out / f"{name}.json").write_text(json.dumps(data, indent=1, sort_keys=True))
+
+
+def logit_stats(got: torch.Tensor, ref: torch.Tensor) -> dict:
+    d = (got.float() - ref.float()).abs()
+    return {"max_abs": round(d.max().item(), 5), "rms": round(d.pow(2).mean().sqrt().item(), 5)}
