@@ -18,12 +18,26 @@ per step / mean step time vs 8 TB/s), and a CPU baseline: the oracle's fp32
 decode step timed on this host's cores on a bounded sample.
 
 ``--config c4`` / ``--config c5`` time the batched step instead (BASELINE
-configs 4 and 5; not the headline line): batch 8 with ragged KV lengths
-(prompt lengths uniform in [512, 3840], seed 0, so that 256 steps fit the
-4096-row caches) and batch 32 at KV lengths 8064..8191 of 8192-row caches.
-Their caches below each sequence's start position hold N(0,1) bf16 values
-instead of prefilled K/V (the step's cost does not depend on the values);
-tok/s counts every sequence's token.
+configs 4 and 5; not the headline line). C4: batch 8 through the model seam
+(``NeuronLlamaForCausalLM`` with batch_size 8), each sequence an independent
+uniform-random prompt of length uniform in [512, 3840] (seed 0, so that 256
+steps fit the 4096-row caches) prefilled on the GPU into its own cache slice,
+then greedy steps at every sequence's own position. C5: batch 32 at KV
+lengths 8064..8191 of 8192-row caches whose rows below each start position
+hold N(0,1) bf16 values instead of prefilled K/V (BASELINE config 5 allows
+this to save 258k tokens of prefill; the step's cost does not depend on the
+values). tok/s counts every sequence's token.
+
+CPU baselines (every config): the oracle's decode step (fp32 accumulation,
+bf16 rounding points; one sequence at a time) timed on the host cores, on a
+bounded sample stated in ``sample``; threads = the CPU share the process may
+use (its affinity mask, capped by ``OMP_NUM_THREADS``, which the GPU pool sets
+to its per-GPU share), with the CPU model string.
+
+``traffic`` is not measured inside a bench run: it is the HBM bytes per step
+of the same kernel and workload from two ``rocprofv3 --pmc`` runs (FETCH_SIZE,
+WRITE_SIZE, scaled by a plain-copy calibration), read from the committed
+``profiles/*_traffic.json`` named in ``traffic_source``.
 
 ``--config c2`` times BASELINE config 2 instead: one decoder layer (layer 0 of
 the seed-0 weights) as its own launch of the decode kernel (``mk_layer_step``
@@ -51,8 +65,12 @@ sys.path.insert(1, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (scaled by the plain-copy calibration); see profiles/mk_decode_kernel_c3_bs1.md
-TRAFFIC_JSON = REPO / "profiles" / "mk_decode_kernel_c3_bs1_traffic.json"
+# (scaled by the plain-copy calibration), one file per kernel and workload
+TRAFFIC_JSON = {
+    "c3": REPO / "profiles" / "mk_decode_kernel_c3_bs1_traffic.json",
+    "c4": REPO / "profiles" / "mk_batch_kernel_c4_traffic.json",
+    "c5": REPO / "profiles" / "mk_batch_kernel_c5_traffic.json",
+}
 PROMPT = 384
 S_MAX = 1024
 BATCH_CONFIGS = {
@@ -99,36 +117,74 @@ def step_latencies(launch, K: int, reset):
     return [evs[i].elapsed_time(evs[i + 1]) for i in range(K)]
 
 
-def cpu_baseline(sd, n_steps: int, budget_s: float):
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the affinity mask, capped by
+    OMP_NUM_THREADS (the GPU pool sets it to the CPU share of one GPU)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def traffic_of(config: str):
+    """(HBM bytes per step, source) from the committed rocprofv3 counter summary, or (None, None)."""
+    f = TRAFFIC_JSON.get(config)
+    if f is None or not f.exists():
+        return None, None
+    return int(json.loads(f.read_text())["traffic_bytes_per_step"]), str(f.relative_to(REPO))
+
+
+def cpu_baseline(sd, positions, s_max: int, steps_per_seq: int, budget_s: float, what: str):
     """The oracle's decode step (fp32 accumulation, bf16 rounding points) on the
-    host cores, at positions 384.. with a synthetic N(0,1) KV cache."""
+    host cores: for each of ``steps_per_seq`` rounds, one step of every
+    sequence in ``positions`` (its start position + round), over one
+    synthetic N(0,1) bf16 cache of ``s_max`` rows (a step reads only rows
+    below its position, so the sequences can share it). Stops early after
+    ``budget_s`` seconds of steps."""
     import torch
     from oracle.llama_ref import OracleLlama
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     t0 = time.perf_counter()
     o = OracleLlama(sd, mode="mk")
     g = torch.Generator().manual_seed(1)
-    cache = [(torch.randn(8, S_MAX, 64, generator=g).to(torch.bfloat16).float(),
-              torch.randn(8, S_MAX, 64, generator=g).to(torch.bfloat16).float()) for _ in range(16)]
-    log(f"[cpu] oracle ready in {time.perf_counter() - t0:.1f}s, {threads} threads")
+    cache = [(torch.randn(8, s_max, 64, generator=g).to(torch.bfloat16).float(),
+              torch.randn(8, s_max, 64, generator=g).to(torch.bfloat16).float()) for _ in range(16)]
+    log(f"[cpu] oracle ready in {time.perf_counter() - t0:.1f}s, {threads} threads ({cpu_model()})")
     tok = torch.tensor([17])
-    o.forward(tok, PROMPT, cache)              # warm-up step
-    times = []
+    o.forward(tok, positions[0], cache)              # warm-up step
+    o.forward(tok, positions[0], cache)
+    times, done = [], []
     t_start = time.perf_counter()
-    for i in range(n_steps):
-        t = time.perf_counter()
-        logits, _ = o.forward(tok, PROMPT + 1 + i, cache)
-        tok = logits.argmax(-1)
-        times.append(time.perf_counter() - t)
+    for r in range(steps_per_seq):
+        for p in positions:
+            t = time.perf_counter()
+            logits, _ = o.forward(tok, p + r, cache)
+            tok = logits.argmax(-1)
+            times.append(time.perf_counter() - t)
+            done.append(p + r)
+            if time.perf_counter() - t_start > budget_s:
+                break
         if time.perf_counter() - t_start > budget_s:
             break
     total = sum(times)
     return {
         "value": round(len(times) / total, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-        "sample": f"{len(times)} oracle decode steps (fp32 accumulation, bf16 rounding points) at positions "
-                  f"{PROMPT + 1}..{PROMPT + len(times)} with a synthetic N(0,1) bf16 KV cache; "
-                  f"p50 {statistics.median(times) * 1e3:.1f} ms/step",
+        "cpu_model": cpu_model(),
+        "sample": f"{len(times)} oracle decode steps ({what}; fp32 accumulation, bf16 rounding points, one "
+                  f"sequence per step) at positions {min(done)}..{max(done)} over a synthetic N(0,1) bf16 KV "
+                  f"cache of {s_max} rows, after 2 warm-up steps; p50 {statistics.median(times) * 1e3:.1f} ms/step",
     }
 
 
@@ -137,8 +193,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-steps", type=int, default=24)
-    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--cpu-steps", type=int, default=48, help="C3 CPU baseline steps (>= 32)")
+    ap.add_argument("--cpu-budget-s", type=float, default=30.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c3",
                     help="c3: the headline bs=1 decode; c2: one decoder layer; c4/c5: the batched configurations")
@@ -217,9 +273,7 @@ def main():
     bytes_per_step = sum(step_bytes(16, [PROMPT + i], lm_head=True) for i in range(K)) / K
     achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
 
-    traffic = None
-    if TRAFFIC_JSON.exists():
-        traffic = int(json.loads(TRAFFIC_JSON.read_text())["traffic_bytes_per_step"])
+    traffic, traffic_src = traffic_of("c3")
     result = {
         "metric": "bs=1 decode tok/s + p50 step latency, Llama-3.2-1B ctx1024; HBM GB/s",
         "value": round(K / wall, 2),
@@ -240,7 +294,7 @@ def main():
                                f"KV cache, greedy steps at KV lengths {PROMPT}..{PROMPT + K - 1}",
                    "batch": 1, "prompt": PROMPT, "max_context_length": S_MAX, "n_layers": 16},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "bytes_per_step": int(bytes_per_step), "kernel": "mk_decode_kernel"},
         "cpu_baseline": None,
     }
@@ -249,7 +303,8 @@ def main():
         torch.cuda.empty_cache()
         from mk_weights import synthetic_state_dict
         sd = synthetic_state_dict(seed=0)
-        result["cpu_baseline"] = cpu_baseline(sd, args.cpu_steps, args.cpu_budget_s)
+        result["cpu_baseline"] = cpu_baseline(sd, [PROMPT + 1], S_MAX, args.cpu_steps, args.cpu_budget_s,
+                                              "C3 shapes, batch 1")
     print(json.dumps(result), flush=True)
 
 
@@ -310,21 +365,23 @@ def run_layer(args):
     if not args.no_cpu_baseline:
         # the oracle's layer on the host cores: timed, and the reference for the max-abs check
         from oracle.llama_ref import Dims, OracleLlama
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        threads = cpu_threads()
         torch.set_num_threads(threads)
         o = OracleLlama(sd, Dims(n_layers=1), mode="mk")
         times, ref = [], None
-        for _ in range(5):
+        for _ in range(22):
             cache = [(k0[0].float().clone(), v0[0].float().clone())]
             t = time.perf_counter()
             _, ref = o.forward(None, POS, cache, hidden=hidden.float(), want_logits=False)
             times.append(time.perf_counter() - t)
+        times = times[2:]                       # 2 warm-up runs
         err = (out.cpu().float() - ref).abs().max().item()
         result["max_abs_err_vs_oracle"] = round(err, 5)
         result["cpu_baseline"] = {
             "value": round(statistics.median(times) * 1e6, 1), "unit": "us", "cores": threads, "kind": "port",
-            "sample": "5 runs of the oracle's decoder layer (fp32 accumulation, bf16 rounding points) at "
-                      f"position {POS}, median",
+            "cpu_model": cpu_model(),
+            "sample": f"{len(times)} runs of the oracle's decoder layer (fp32 accumulation, bf16 rounding "
+                      f"points) at position {POS} after 2 warm-up runs, median",
         }
     print(json.dumps(result), flush=True)
 
@@ -334,27 +391,58 @@ def run_batched(args, cfg):
     import torch
     import mk_lib
     from mk_config import LLAMA_3_2_1B, step_bytes
-    from mk_weights import pack_for_megakernel, random_token_ids, synthetic_state_dict
+    from mk_weights import random_token_ids
 
     B, S, K = cfg["batch"], cfg["s_max"], min(args.steps, cfg["steps"])
     g = torch.Generator().manual_seed(0)
-    starts = [int(torch.randint(cfg["lo"], cfg["hi"] + 1, (1,), generator=g)) for _ in range(B)]
+    lens = [int(torch.randint(cfg["lo"], cfg["hi"] + 1, (1,), generator=g)) for _ in range(B)]
     t0 = time.perf_counter()
-    sd = synthetic_state_dict(seed=0)
-    packed = pack_for_megakernel(sd, LLAMA_3_2_1B, device="cuda", rope_rows=S)
-    del sd
-    w = mk_lib.weights_struct(packed)
-    # caches: N(0,1) bf16 (rows at and above a sequence's start are rewritten by the steps)
-    kv = torch.empty(16, 2, B, 8, S, 64, dtype=torch.bfloat16, device="cuda")
-    gd = torch.Generator(device="cuda").manual_seed(1)
-    for l in range(16):
-        kv[l].normal_(generator=gd)
-    ws = mk_lib.Workspace(B, S, torch.device("cuda"))
-    pos = torch.tensor(starts, dtype=torch.int32, device="cuda")
-    toks = random_token_ids(B, seed=0).to(device="cuda", dtype=torch.int32)
-    logits = torch.empty(B, LLAMA_3_2_1B.vocab, dtype=torch.float32, device="cuda")
-    step = mk_lib.StepLauncher(w, ws, [kv[l, 0] for l in range(16)], [kv[l, 1] for l in range(16)], pos,
-                               tokens=toks, logits=logits, next_token=toks, flags=mk_lib.MK_FLAG_ADVANCE, batch=B)
+    prefill_ms = None
+    if args.config == "c4":
+        # the model seam: one prompt per sequence, prefilled on the GPU into its own cache slice
+        from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
+        model = NeuronLlamaForCausalLM("random:0", LlamaInferenceConfig(
+            NeuronConfigLlamaMK(batch_size=B, seq_len=S, max_context_length=S)))
+        model.compile()
+        model.load()
+        sd = model.state_dict_bf16
+        prompts = [random_token_ids(n, seed=100 + b) for b, n in enumerate(lens)]
+        model.prefill(prompts)                       # warm-up (allocates the prefill workspace)
+        torch.cuda.synchronize()
+        tp = time.perf_counter()
+        model.prefill(prompts)
+        torch.cuda.synchronize()
+        prefill_ms = (time.perf_counter() - tp) * 1e3
+        if model.prefill_device_error():
+            sys.exit("device error in the prefill steps")
+        step, ws, pos, toks = model.launcher("decode"), model.ws, model.pos, model.tokens
+        starts = [n - 1 for n in lens]
+        data = ("synthetic (random-init N(0,0.02) bf16 weights seed 0; one uniform-random prompt per sequence, "
+                "prefilled on the GPU)")
+        workload = (f"C4: Llama-3.2-1B decode, batch 8, independent prompts of lengths {min(lens)}..{max(lens)} "
+                    f"prefilled into {S}-row KV caches, {K} greedy steps")
+    else:
+        from mk_weights import pack_for_megakernel, synthetic_state_dict
+        sd = synthetic_state_dict(seed=0)
+        packed = pack_for_megakernel(sd, LLAMA_3_2_1B, device="cuda", rope_rows=S)
+        w = mk_lib.weights_struct(packed)
+        # caches: N(0,1) bf16 (rows at and above a sequence's start are rewritten by the steps)
+        kv = torch.empty(16, 2, B, 8, S, 64, dtype=torch.bfloat16, device="cuda")
+        gd = torch.Generator(device="cuda").manual_seed(1)
+        for l in range(16):
+            kv[l].normal_(generator=gd)
+        ws = mk_lib.Workspace(B, S, torch.device("cuda"))
+        starts = lens
+        pos = torch.tensor(starts, dtype=torch.int32, device="cuda")
+        toks = random_token_ids(B, seed=0).to(device="cuda", dtype=torch.int32)
+        logits = torch.empty(B, LLAMA_3_2_1B.vocab, dtype=torch.float32, device="cuda")
+        step = mk_lib.StepLauncher(w, ws, [kv[l, 0] for l in range(16)], [kv[l, 1] for l in range(16)], pos,
+                                   tokens=toks, logits=logits, next_token=toks, flags=mk_lib.MK_FLAG_ADVANCE,
+                                   batch=B)
+        data = ("synthetic (random-init N(0,0.02) bf16 weights seed 0, N(0,1) bf16 KV cache below each start "
+                "position, uniform-random token ids)")
+        workload = (f"C5: Llama-3.2-1B decode, batch {B}, {S}-row KV caches, start positions "
+                    f"{min(starts)}..{max(starts)}, {K} greedy steps")
     torch.cuda.synchronize()
     log(f"[bench] {args.config}: batch {B}, cache rows {S}, start positions {min(starts)}..{max(starts)}; "
         f"ready in {time.perf_counter() - t0:.1f}s")
@@ -377,6 +465,7 @@ def run_batched(args, cfg):
         sys.exit(f"device error bits 0x{bits:x}")
     bytes_per_step = sum(step_bytes(16, [p + i for p in starts], lm_head=True) for i in range(K)) / K
     achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
+    traffic, traffic_src = traffic_of(args.config)
     result = {
         "metric": f"batched decode tok/s (all sequences), Llama-3.2-1B, {args.config.upper()}; HBM GB/s",
         "value": round(B * K / wall, 2),
@@ -387,21 +476,30 @@ def run_batched(args, cfg):
         "ms_per_step": round(wall * 1e3 / K, 4),
         "p50_step_ms": round(statistics.median(step_ms), 4),
         "p90_step_ms": round(sorted(step_ms)[int(0.9 * (K - 1))], 4),
+        "prefill_ms": None if prefill_ms is None else round(prefill_ms, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init N(0,0.02) bf16 weights seed 0, N(0,1) bf16 KV cache below each start "
-                "position, uniform-random token ids)",
-        "config": {"workload": f"{args.config.upper()}: Llama-3.2-1B decode, batch {B}, {S}-row KV caches, "
-                               f"start positions {min(starts)}..{max(starts)}, {K} greedy steps",
-                   "batch": B, "max_context_length": S, "start_positions": starts, "n_layers": 16},
+        "data": data,
+        "config": {"workload": workload, "batch": B, "max_context_length": S, "start_positions": starts,
+                   "n_layers": 16},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "bytes_per_step": int(bytes_per_step),
                      "kernel": f"mk_batch_kernel<{1 if B <= 16 else 2}>"},
         "cpu_baseline": None,
     }
+    if not args.no_cpu_baseline:
+        if args.config == "c4":
+            del model
+        torch.cuda.empty_cache()
+        if args.config == "c4":
+            result["cpu_baseline"] = cpu_baseline(sd, starts, S, 2, args.cpu_budget_s,
+                                                  "C4 shapes: each of the 8 sequences' start positions, 2 rounds")
+        else:
+            result["cpu_baseline"] = cpu_baseline(sd, starts[::8], S, 4, args.cpu_budget_s,
+                                                  "C5 shapes: 4 of the 32 sequences' start positions, 4 rounds")
     print(json.dumps(result), flush=True)
 
 

@@ -121,48 +121,59 @@ class NeuronLlamaForCausalLMMK:
         if self.packed is None:
             self.compile(compiled_model_path)
         nc, d = self.neuron_config, self.config.dims
-        if nc.batch_size != 1:
-            raise NotImplementedError("this build runs batch 1")
+        B = nc.batch_size
+        if not 1 <= B <= mk_lib.PREFILL_CHUNK:
+            raise ValueError(f"batch_size {B} not in [1, {mk_lib.PREFILL_CHUNK}]")
         dev = torch.device(nc.device)
+        self.batch_size = B
         self.s_max = nc.max_context_length
-        # past_key_values: one [1, 8, S, 64] K and V tensor per layer, views of one allocation
-        self.kv = torch.zeros(d.n_layers, 2, nc.batch_size, d.n_kv_heads, self.s_max, d.head_dim,
+        # past_key_values: one [B, 8, S, 64] K and V tensor per layer, views of one allocation;
+        # sequence b's rows of layer l are kv[l, :, b] (its own slice: no padding between sequences)
+        self.kv = torch.zeros(d.n_layers, 2, B, d.n_kv_heads, self.s_max, d.head_dim,
                               dtype=torch.bfloat16, device=dev)
         self.k_caches = [self.kv[l, 0] for l in range(d.n_layers)]
         self.v_caches = [self.kv[l, 1] for l in range(d.n_layers)]
         self.weights = mk_lib.weights_struct(self.packed)
-        self.ws = mk_lib.Workspace(nc.batch_size, self.s_max, dev)
-        self.pos = torch.zeros(nc.batch_size, dtype=torch.int32, device=dev)
-        self.tokens = torch.zeros(nc.batch_size, dtype=torch.int32, device=dev)
-        self.logits = torch.zeros(nc.batch_size, d.vocab, dtype=torch.float32, device=dev)
-        self.hidden_out = torch.zeros(nc.batch_size, d.hidden, dtype=torch.bfloat16, device=dev)
+        # batch 1 runs the GEMV kernel; batches of 2..32 the MFMA kernel
+        self.ws = mk_lib.Workspace(B, self.s_max, dev)
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.logits = torch.zeros(B, d.vocab, dtype=torch.float32, device=dev)
+        self.hidden_out = torch.zeros(B, d.hidden, dtype=torch.bfloat16, device=dev)
         self.pf_ws: Optional[mk_lib.Workspace] = None   # batched workspace of the prefill steps (on first use)
+        self.ws1: Optional[mk_lib.Workspace] = None     # batch-1 workspace of token-by-token prefill (B > 1)
         self.pf_pos = torch.arange(self.s_max, dtype=torch.int32, device=dev)
         self._ready = True
         self._launchers: Dict[str, mk_lib.StepLauncher] = {}
 
     def reset(self) -> None:
-        """Start a new sequence (rows >= pos are never read, so no cache clear)."""
+        """Start new sequences (rows >= pos are never read, so no cache clear)."""
         self.pos.zero_()
 
     @property
     def past_key_values(self) -> List[Tuple[torch.Tensor, torch.Tensor]]:
         return list(zip(self.k_caches, self.v_caches))
 
+    def seq_caches(self, b: int) -> Tuple[List[torch.Tensor], List[torch.Tensor]]:
+        """Per-layer K and V caches of sequence b alone ([1, 8, S, 64] views)."""
+        return ([self.kv[l, 0, b:b + 1] for l in range(self.kv.shape[0])],
+                [self.kv[l, 1, b:b + 1] for l in range(self.kv.shape[0])])
+
     # -- steps ---------------------------------------------------------------
     def launcher(self, kind: str) -> mk_lib.StepLauncher:
-        """Prebuilt steps on the current stream:
+        """Prebuilt steps over the whole batch on the current stream:
         "prefill": token in, K/V written, pos += 1, no lm_head;
         "decode":  token in, logits + greedy next token written back into the
-                   token buffer, pos += 1 (autoregressive loop on device)."""
+                   token buffer, pos += 1 (autoregressive loop on device);
+        "decode_logits": logits only (the next token comes from mk_sample)."""
         if kind not in self._launchers:
-            common = dict(pos=self.pos, tokens=self.tokens, flags=mk_lib.MK_FLAG_ADVANCE)
+            common = dict(pos=self.pos, tokens=self.tokens, flags=mk_lib.MK_FLAG_ADVANCE, batch=self.batch_size)
             if kind == "prefill":
                 l = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, **common)
             elif kind == "decode":
                 l = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, logits=self.logits,
                                         next_token=self.tokens, hidden_out=self.hidden_out, **common)
-            elif kind == "decode_logits":   # logits only: the next token comes from mk_sample
+            elif kind == "decode_logits":
                 l = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, logits=self.logits,
                                         hidden_out=self.hidden_out, **common)
             else:
@@ -177,9 +188,11 @@ class NeuronLlamaForCausalLMMK:
 
         ``input_ids`` [B] / [B, 1] int token ids, or ``hidden_states`` [B, 1, H]
         bf16 (the layer-0 input of the reference contract); ``position_ids`` [B]
-        or [B, 1] — the row the fresh K/V is written to. ``past_key_values``
-        defaults to the model's own caches; the returned caches are the same
-        tensors, updated in place.
+        or [B, 1] — the row each sequence's fresh K/V is written to (sequences
+        may sit at different positions). ``past_key_values`` defaults to the
+        model's own caches ([B, 8, S, 64] per layer); the returned caches are
+        the same tensors, updated in place. B may be smaller than the loaded
+        batch size: the first B sequences of the caches step.
         """
         assert self._ready, "call load() first"
         kv = past_key_values if past_key_values is not None else self.past_key_values
@@ -189,62 +202,110 @@ class NeuronLlamaForCausalLMMK:
         pos = position_ids.reshape(-1).to(device=dev, dtype=torch.int32)
         toks = None if input_ids is None else input_ids.reshape(-1).to(device=dev, dtype=torch.int32)
         hid = None if hidden_states is None else hidden_states.reshape(-1, self.config.dims.hidden).to(dev)
+        nb = int(pos.numel())
+        if not 1 <= nb <= self.batch_size:
+            raise ValueError(f"{nb} positions for a model loaded with batch_size {self.batch_size}")
         mk_lib.decode_step(self.weights, self.ws, ks, vs, pos, tokens=toks, hidden_in=hid,
-                           logits=self.logits, next_token=self.tokens)
-        return self.logits, kv
+                           logits=self.logits[:nb], next_token=self.tokens[:nb], batch=nb)
+        return self.logits[:nb], kv
+
+    def _prompts(self, input_ids) -> List[torch.Tensor]:
+        """The batch's prompts as 1-D tensors: [n] (batch 1), [B, n], or a list
+        of B 1-D tensors of their own lengths (no padding: every sequence has
+        its own cache slice and position)."""
+        if isinstance(input_ids, torch.Tensor):
+            ps = [input_ids.reshape(-1)] if input_ids.dim() <= 1 else list(input_ids)
+        else:
+            ps = [torch.as_tensor(p).reshape(-1) for p in input_ids]
+        if len(ps) != self.batch_size:
+            raise ValueError(f"{len(ps)} prompts for a model loaded with batch_size {self.batch_size}")
+        for p in ps:
+            if not 1 <= int(p.numel()) <= self.s_max:
+                raise ValueError(f"prompt of {int(p.numel())} tokens does not fit max_context_length {self.s_max}")
+        return ps
 
     @torch.no_grad()
-    def prefill(self, prompt: torch.Tensor, batched: bool = True) -> None:
-        """Write the K/V rows of prompt tokens 0..n-2 (positions 0..n-2); leaves
-        the last prompt token in the token buffer and pos = n - 1, so the next
-        decode step processes it and yields the first generated token.
+    def prefill(self, prompt, batched: bool = True) -> None:
+        """For each sequence b, write the K/V rows of its prompt tokens 0..n_b-2
+        into its own cache slice; leaves its last prompt token in the token
+        buffer and pos[b] = n_b - 1, so the next decode step processes it and
+        yields the first generated token.
 
-        batched: chunks of up to 32 tokens per launch of the batched kernel
-        (MK_FLAG_PREFILL); otherwise one decode-kernel launch per token."""
+        batched: chunks of up to 32 consecutive tokens of one sequence per launch
+        of the batched kernel (MK_FLAG_PREFILL); otherwise one decode-kernel
+        launch per token."""
+        prompts = self._prompts(prompt)
         self.reset()
-        n = int(prompt.numel())
-        if n < 1 or n > self.s_max:
-            raise ValueError(f"prompt of {n} tokens does not fit max_context_length {self.s_max}")
-        prompt_dev = prompt.reshape(-1).to(device=self.pos.device, dtype=torch.int32)
-        if batched:
-            if self.pf_ws is None:
-                self.pf_ws = mk_lib.Workspace(mk_lib.PREFILL_CHUNK, self.s_max, self.pos.device)
-            for c0 in range(0, n - 1, mk_lib.PREFILL_CHUNK):
-                m = min(mk_lib.PREFILL_CHUNK, n - 1 - c0)
-                mk_lib.decode_step(self.weights, self.pf_ws, self.k_caches, self.v_caches, self.pf_pos[c0:c0 + m],
-                                   tokens=prompt_dev[c0:c0 + m], flags=mk_lib.MK_FLAG_PREFILL, batch=m)
-            self.pos.fill_(n - 1)
-        else:
-            pf = self.launcher("prefill")
-            for i in range(n - 1):
-                self.tokens.copy_(prompt_dev[i:i + 1])
-                pf.launch()
-        self.tokens.copy_(prompt_dev[n - 1:n])
+        dev = self.pos.device
+        last = []
+        for b, p in enumerate(prompts):
+            n = int(p.numel())
+            prompt_dev = p.to(device=dev, dtype=torch.int32)
+            kc, vc = self.seq_caches(b)
+            if batched:
+                if self.pf_ws is None:
+                    self.pf_ws = mk_lib.Workspace(mk_lib.PREFILL_CHUNK, self.s_max, dev)
+                for c0 in range(0, n - 1, mk_lib.PREFILL_CHUNK):
+                    m = min(mk_lib.PREFILL_CHUNK, n - 1 - c0)
+                    mk_lib.decode_step(self.weights, self.pf_ws, kc, vc, self.pf_pos[c0:c0 + m],
+                                       tokens=prompt_dev[c0:c0 + m], flags=mk_lib.MK_FLAG_PREFILL, batch=m)
+            elif self.batch_size == 1:
+                pf = self.launcher("prefill")
+                for i in range(n - 1):
+                    self.tokens.copy_(prompt_dev[i:i + 1])
+                    pf.launch()
+            else:
+                if self.ws1 is None:
+                    self.ws1 = mk_lib.Workspace(1, self.s_max, dev)
+                pos1 = torch.zeros(1, dtype=torch.int32, device=dev)
+                tok1 = torch.zeros(1, dtype=torch.int32, device=dev)
+                pf = mk_lib.StepLauncher(self.weights, self.ws1, kc, vc, pos1, tokens=tok1,
+                                         flags=mk_lib.MK_FLAG_ADVANCE)
+                for i in range(n - 1):
+                    tok1.copy_(prompt_dev[i:i + 1])
+                    pf.launch()
+            last.append(prompt_dev[n - 1:n])
+        self.pos.copy_(torch.tensor([int(p.numel()) - 1 for p in prompts], dtype=torch.int32))
+        self.tokens.copy_(torch.cat(last))
 
     def prefill_device_error(self) -> int:
         """Device error bits of the prefill steps since the last call (0 = none)."""
-        return 0 if self.pf_ws is None else self.pf_ws.read_device_error()
+        bits = 0
+        for ws in (self.pf_ws, self.ws1):
+            if ws is not None:
+                bits |= ws.read_device_error()
+        return bits
+
+    def _sampling_rows(self, sampling_params: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if sampling_params is None:
+            return None
+        sp = sampling_params.to(device=self.pos.device, dtype=torch.float32).reshape(-1, 3)
+        if sp.shape[0] == 1 and self.batch_size > 1:
+            sp = sp.expand(self.batch_size, 3)
+        if sp.shape[0] != self.batch_size:
+            raise ValueError(f"sampling parameters for {sp.shape[0]} rows, batch {self.batch_size}")
+        return sp.contiguous()
 
     @torch.no_grad()
     def decode_graph(self, n_steps: int, sampling_params: Optional[torch.Tensor] = None, seed: int = 0):
-        """Capture ``n_steps`` consecutive decode steps (each followed by the
-        on-device sampler if ``sampling_params`` is given) into one HIP graph.
+        """Capture ``n_steps`` consecutive decode steps of the whole batch (each
+        followed by the on-device sampler if ``sampling_params`` is given) into
+        one HIP graph.
 
-        Every step reads its token and position from the device and writes
+        Every step reads its tokens and positions from the device and writes
         them back (MK_FLAG_ADVANCE), so a replay continues from whatever state
         the model is in — e.g. right after ``prefill`` — exactly as the same
-        launches issued one by one; the step's token is also appended to
-        ``self.graph_tokens[:n_steps]``. The graph runs on a private stream;
+        launches issued one by one; step i's tokens are also written to
+        ``self.graph_tokens[i]``. The graph runs on a private stream;
         ``replay()`` orders it after the current stream's work."""
-        if sampling_params is not None:
-            sampling_params = sampling_params.to(device=self.pos.device, dtype=torch.float32).reshape(1, 3)
+        sampling_params = self._sampling_rows(sampling_params)
         stream = torch.cuda.Stream(device=self.pos.device)
         kw = dict(pos=self.pos, tokens=self.tokens, flags=mk_lib.MK_FLAG_ADVANCE, logits=self.logits,
-                  hidden_out=self.hidden_out, stream=stream)
+                  hidden_out=self.hidden_out, stream=stream, batch=self.batch_size)
         if sampling_params is None:
             kw["next_token"] = self.tokens
         step = mk_lib.StepLauncher(self.weights, self.ws, self.k_caches, self.v_caches, **kw)
-        self.graph_tokens = torch.zeros(n_steps, dtype=torch.int32, device=self.pos.device)
+        self.graph_tokens = torch.zeros(n_steps, self.batch_size, dtype=torch.int32, device=self.pos.device)
         graph = torch.cuda.CUDAGraph()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
@@ -252,43 +313,50 @@ class NeuronLlamaForCausalLMMK:
                 step.launch()
                 if sampling_params is not None:
                     mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
-                self.graph_tokens[i:i + 1].copy_(self.tokens)
+                self.graph_tokens[i].copy_(self.tokens)
         graph._mk_keep = (step, sampling_params, stream)
         return graph
 
     @torch.no_grad()
-    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, return_logits: bool = False,
+    def generate(self, input_ids, max_new_tokens: int, return_logits: bool = False,
                  sampling_params: Optional[torch.Tensor] = None, seed: int = 0):
-        """Generation for one sequence: returns the new token ids (and the
-        per-step fp32 logits if requested). Greedy (the decode kernel's argmax)
-        unless ``sampling_params`` [1, 3] (top_k, top_p, temperature) is given:
-        then each step's logits go through the on-device sampler, whose Philox
-        counter is the position of the token being produced (reproducible for
-        a given seed)."""
-        prompt = input_ids.reshape(-1)
-        n = int(prompt.numel())
-        if n + max_new_tokens - 1 > self.s_max:
-            raise ValueError(f"{n} + {max_new_tokens} tokens exceed max_context_length {self.s_max}")
-        self.prefill(prompt)
+        """Generation for the batch's sequences (prompts as in ``prefill``):
+        returns the new token ids, [max_new_tokens] for a 1-D prompt of a
+        batch-1 model, else [B, max_new_tokens] (and the per-step fp32 logits,
+        [steps, V] or [B, steps, V], if requested). Greedy (the kernel's argmax)
+        unless ``sampling_params`` ([1, 3] or [B, 3]: top_k, top_p,
+        temperature) is given: then each step's logits go through the
+        on-device sampler, whose Philox counter is the position of the token
+        being produced (reproducible for a given seed)."""
+        prompts = self._prompts(input_ids)
+        for p in prompts:
+            if int(p.numel()) + max_new_tokens - 1 > self.s_max:
+                raise ValueError(f"{int(p.numel())} + {max_new_tokens} tokens exceed max_context_length {self.s_max}")
+        self.prefill(prompts)
         dec = self.launcher("decode" if sampling_params is None else "decode_logits")
-        if sampling_params is not None:
-            sampling_params = sampling_params.to(device=self.pos.device, dtype=torch.float32).reshape(1, 3)
-        out = torch.empty(max_new_tokens, dtype=torch.int32, device=self.pos.device)
+        sampling_params = self._sampling_rows(sampling_params)
+        B = self.batch_size
+        out = torch.empty(max_new_tokens, B, dtype=torch.int32, device=self.pos.device)
         logits = [] if return_logits else None
         for t in range(max_new_tokens):
             dec.launch()
             if sampling_params is not None:
                 mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
-            out[t:t + 1].copy_(self.tokens)
+            out[t].copy_(self.tokens)
             if return_logits:
                 logits.append(self.logits.clone())
         torch.cuda.synchronize()
         bits = self.ws.read_device_error() | self.prefill_device_error()
         if bits:
             raise RuntimeError(f"megakernel device error bits 0x{bits:x}")
-        if return_logits:
-            return out.cpu(), torch.cat(logits).cpu()
-        return out.cpu()
+        flat = B == 1 and isinstance(input_ids, torch.Tensor) and input_ids.dim() <= 1
+        toks = out.t().cpu()
+        if flat:
+            toks = toks[0]
+        if not return_logits:
+            return toks
+        lg = torch.stack(logits, 1).cpu()      # [B, steps, V]
+        return toks, (lg[0] if flat else lg)
 
 
 # Symbol main.py imports when --enable-nki is set (llama_with_megakernel.py:355).

@@ -1,36 +1,51 @@
 """Driver with the reference's CLI (main.py:34-105, 538-669) for this build.
 
-  python main.py --mode generate [--enable-nki] [--prompt-ids 1,2,3 | --prompt-len 384]
-                 [--max-new-tokens N] [--model-path random:0 | /path/to/hf_checkpoint]
+  python main.py --mode generate [--enable-nki] [--prompt TEXT ... | --prompt-ids 1,2,3 ... | --prompt-len 384]
+                 [--max-new-tokens N] [--model-path random:0 | /path/to/hf_checkpoint] [--tokenizer-path DIR]
   python main.py --mode validate --enable-nki [...]
   python main.py --mode benchmark --enable-nki [...]
 
-* generate: greedy generation with the megakernel model (the reference's
-  run_generation, main.py:360-375). Prompts are token ids (no tokenizer or
-  network here); ``--tokenizer-path`` decodes the output if a local tokenizer
-  is given.
+Prompts. As in the reference (main.py:56, 538-540) every ``--prompt`` is one
+sequence of the batch and the batch size is their number. Text prompts are
+encoded with the checkpoint's own tokenizer, read from a local directory only
+(``--tokenizer-path``, default ``--model-path``; the reference's
+load_tokenizer, main.py:114-118, with the pad token set to EOS). The
+reference pads a batch of prompts to one length (main.py:217, 277); here each
+sequence has its own cache slice and position, so prompts keep their own
+lengths and need no padding or attention mask (the same positions and causal
+attention a left-padded, masked sequence sees). ``--prompt-ids`` gives a
+prompt as token ids instead (repeatable); with no prompt at all,
+``--batch-size`` random prompts of ``--prompt-len`` ids are drawn (seeds 0..).
+
+* generate: generation with the megakernel model (the reference's
+  run_generation, main.py:360-375), greedy unless --top-k/--top-p/--temperature
+  ask for on-device sampling; with a tokenizer the outputs are decoded.
 * validate: the megakernel model against the stock PyTorch path
   (llama_baseline.StockLlama, fp32) on the same weights and token ids, with
   teacher forcing after a divergence as in check_accuracy_logits
   (main.py:274-357): per-step logit error and greedy agreement; the criteria
-  are those of tests/test_gpu_decode.py (bf16 noise floor, see there).
+  are those of tests/test_gpu_decode.py (bf16 noise floor, see there). The
+  reference's tol_map and divergence tolerance (main.py:51, 542) are reported
+  as restated checks (mk_validate).
 * benchmark: e2e / context-encoding / token-generation latency percentiles and
   throughput in the shape of NxDI's benchmark report (main.py:178-271),
   written to benchmark_report.json.
 
 ``--enable-nki`` selects the megakernel model (llama_with_megakernel), as in
-the reference (main.py:546-553); without it generate/benchmark run the stock
-path. ``--tp-degree`` must be 1 (llama_with_megakernel.py:147-150).
+the reference (main.py:546-553); without it generate runs the stock path.
+``--tp-degree`` must be 1 (llama_with_megakernel.py:147-150).
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import os
 import statistics
 import sys
 import time
 from pathlib import Path
+from typing import List, Optional
 
 import torch
 
@@ -44,13 +59,16 @@ def parse_args(argv=None):
     ap.add_argument("--mode", choices=["generate", "validate", "benchmark"], required=True)
     ap.add_argument("--enable-nki", action="store_true")
     ap.add_argument("--model-path", default="random:0")
-    ap.add_argument("--tokenizer-path", default=None)
-    ap.add_argument("--prompt-ids", default=None, help="comma-separated token ids")
-    ap.add_argument("--prompt-len", type=int, default=384, help="random prompt length (seed 0) if no ids")
+    ap.add_argument("--tokenizer-path", default=None,
+                    help="local tokenizer directory (default: --model-path when it is a directory)")
+    ap.add_argument("--prompt", dest="prompts", action="append", default=None, help="text prompt (repeatable)")
+    ap.add_argument("--prompt-ids", action="append", default=None,
+                    help="comma-separated token ids of one prompt (repeatable)")
+    ap.add_argument("--prompt-len", type=int, default=384, help="random prompt length (seed 0) if no prompt")
     ap.add_argument("--max-new-tokens", type=int, default=640)
     ap.add_argument("--seq-len", type=int, default=1024)
     ap.add_argument("--max-context-length", type=int, default=None)
-    ap.add_argument("--batch-size", type=int, default=1)
+    ap.add_argument("--batch-size", type=int, default=1, help="random prompts drawn when no prompt is given")
     ap.add_argument("--tp-degree", type=int, default=1)
     ap.add_argument("--top-k", type=int, default=1)
     ap.add_argument("--top-p", type=float, default=1.0)
@@ -64,18 +82,52 @@ def parse_args(argv=None):
     ap.add_argument("--graph", action="store_true", help="benchmark: replay the decode steps as one HIP graph")
     ap.add_argument("--num-runs", type=int, default=5)
     ap.add_argument("--num-tokens-to-check", type=int, default=None)
+    ap.add_argument("--report-path", default=BENCHMARK_REPORT_FILENAME)
     return ap.parse_args(argv)
 
 
-def prompt_ids(args):
-    from mk_weights import random_token_ids
-    if args.prompt_ids:
-        return torch.tensor([int(x) for x in args.prompt_ids.split(",")], dtype=torch.int64)
-    return random_token_ids(args.prompt_len, seed=0)
+def tokenizer_dir(args) -> Optional[str]:
+    if args.tokenizer_path:
+        return args.tokenizer_path
+    if not args.model_path.startswith("random:") and os.path.isdir(args.model_path):
+        return args.model_path
+    return None
 
 
-def sampling_params(args):
-    """[1, 3] device tensor (top_k, top_p, temperature), or None for greedy
+def load_tokenizer(path: str):
+    """The checkpoint's tokenizer from a local directory (main.py:114-118):
+    no network, pad token = EOS."""
+    from transformers import AutoTokenizer
+    tok = AutoTokenizer.from_pretrained(path, local_files_only=True)
+    if tok.pad_token is None:
+        tok.pad_token = tok.eos_token
+    return tok
+
+
+def encode_prompts(args, tokenizer=None) -> List[torch.Tensor]:
+    """The batch's prompts as 1-D int64 token-id tensors (see the module doc)."""
+    prompts: List[torch.Tensor] = []
+    if args.prompts:
+        if tokenizer is None:
+            d = tokenizer_dir(args)
+            if d is None:
+                raise SystemExit("--prompt needs a tokenizer: give --tokenizer-path (a local directory)")
+            tokenizer = load_tokenizer(d)
+        for text in args.prompts:
+            ids = tokenizer(text)["input_ids"]
+            if not ids:
+                raise SystemExit(f"prompt {text!r} encodes to no tokens")
+            prompts.append(torch.tensor(ids, dtype=torch.int64))
+    for s in args.prompt_ids or []:
+        prompts.append(torch.tensor([int(x) for x in s.split(",")], dtype=torch.int64))
+    if not prompts:
+        from mk_weights import random_token_ids
+        prompts = [random_token_ids(args.prompt_len, seed=b) for b in range(args.batch_size)]
+    return prompts
+
+
+def sampling_params(args, batch: int = 1):
+    """[B, 3] device tensor (top_k, top_p, temperature), or None for greedy
     (top_k == 1 or do_sample false), as the reference's generation config."""
     import mk_lib
     if not args.do_sample or args.top_k == 1:
@@ -85,94 +137,105 @@ def sampling_params(args):
     k = args.top_k
     if args.global_topk is not None and (k <= 0 or k > args.global_topk):
         k = args.global_topk
-    return mk_lib.prepare_sampling_params(1, k, args.top_p, args.temperature)
+    return mk_lib.prepare_sampling_params(batch, k, args.top_p, args.temperature)
 
 
-def prepare_inference(args):
+def prepare_inference(args, batch: int):
+    """Model construction, compile (weight packing) and load, timed as the
+    reference's prepare_inference does (main.py:121-175); batch_size is the
+    number of prompts (main.py:538-540)."""
     from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
-    nc = NeuronConfigLlamaMK(batch_size=args.batch_size, seq_len=args.seq_len,
+    nc = NeuronConfigLlamaMK(batch_size=batch, seq_len=args.seq_len,
                              max_context_length=args.max_context_length or args.seq_len,
                              tp_degree=args.tp_degree)
     model = NeuronLlamaForCausalLM(args.model_path, LlamaInferenceConfig(nc))
     t0 = time.monotonic()
     model.compile()
     model.load()
-    print(f"model ready in {time.monotonic() - t0:.1f}s (weights packed on the GPU)", flush=True)
+    print(f"model ready in {time.monotonic() - t0:.1f}s (weights packed on the GPU), batch {batch}", flush=True)
     return model
 
 
-def decode_text(args, ids):
-    if not args.tokenizer_path:
-        return None
-    from transformers import AutoTokenizer
-    tok = AutoTokenizer.from_pretrained(args.tokenizer_path, local_files_only=True)
-    return tok.decode(ids)
+def _state_dict(args):
+    from mk_weights import load_hf_checkpoint, synthetic_state_dict
+    if args.model_path.startswith("random:"):
+        return synthetic_state_dict(int(args.model_path.split(":")[1] or 0))
+    return load_hf_checkpoint(args.model_path)
 
 
 def run_generation(args):
-    ids = prompt_ids(args)
+    d = tokenizer_dir(args)
+    tokenizer = load_tokenizer(d) if d else None
+    prompts = encode_prompts(args, tokenizer)
+    B = len(prompts)
     if args.enable_nki:
-        model = prepare_inference(args)
-        out = model.generate(ids, args.max_new_tokens, sampling_params=sampling_params(args), seed=args.seed)
+        model = prepare_inference(args, B)
+        out = model.generate(prompts, args.max_new_tokens, sampling_params=sampling_params(args, B), seed=args.seed)
     else:
         if sampling_params(args) is not None:
             raise SystemExit("the stock path decodes greedily; sampling needs --enable-nki")
         from llama_baseline import StockLlama
-        from mk_weights import load_hf_checkpoint, synthetic_state_dict
-        sd = (synthetic_state_dict(int(args.model_path.split(":")[1] or 0)) if args.model_path.startswith("random:")
-              else load_hf_checkpoint(args.model_path))
-        base = StockLlama(sd, s_max=args.seq_len)
-        for p in range(len(ids) - 1):
-            base.step(int(ids[p]), p)
-        tok, out = int(ids[-1]), []
-        for t in range(args.max_new_tokens):
-            tok = int(base.step(tok, len(ids) - 1 + t).argmax())
-            out.append(tok)
-        out = torch.tensor(out)
-    print("Generated token ids:", out.tolist())
-    text = decode_text(args, out.tolist())
-    if text is not None:
-        print("Generated text:", text)
+        base = StockLlama(_state_dict(args), s_max=args.seq_len)
+        rows = []
+        for ids in prompts:
+            for p in range(len(ids) - 1):
+                base.step(int(ids[p]), p)
+            tok, row = int(ids[-1]), []
+            for t in range(args.max_new_tokens):
+                tok = int(base.step(tok, len(ids) - 1 + t).argmax())
+                row.append(tok)
+            rows.append(row)
+        out = torch.tensor(rows)
+    for b in range(B):
+        print(f"Output {b}: token ids {out[b].tolist()}")
+        if tokenizer is not None:
+            print(f"Output {b}: {tokenizer.decode(out[b].tolist(), skip_special_tokens=True)!r}")
     return out
 
 
 def run_accuracy_check(args) -> bool:
     from llama_baseline import StockLlama
-    ids = prompt_ids(args)
-    model = prepare_inference(args)
-    toks, logits = model.generate(ids, args.max_new_tokens, return_logits=True)
+    from mk_validate import REFERENCE_DIVERGENCE_TOL, divergences, topk_tolerance
+    d = tokenizer_dir(args)
+    prompts = encode_prompts(args, load_tokenizer(d) if d else None)
+    model = prepare_inference(args, len(prompts))
+    toks, logits = model.generate(prompts, args.max_new_tokens, return_logits=True)   # [B, T], [B, T, V]
     n_check = args.num_tokens_to_check or args.max_new_tokens
     base = StockLlama(model.state_dict_bf16, s_max=model.s_max)
-    seq = torch.cat([ids, toks.long()])
-    for p in range(len(ids) - 1):
-        base.step(int(seq[p]), p)
     agree, decided, decided_ok, worst, worst_rms, first_div = 0, 0, 0, 0.0, 0.0, None
-    refs = []
-    for t in range(n_check):
-        ref = base.step(int(seq[len(ids) - 1 + t]), len(ids) - 1 + t).cpu()
-        refs.append(ref)
-        d = (logits[t] - ref).abs()
-        worst = max(worst, d.max().item())
-        worst_rms = max(worst_rms, d.pow(2).mean().sqrt().item())
-        same = int(ref.argmax()) == int(toks[t])
-        agree += same
-        if not same and first_div is None:
-            first_div = t
-        top2 = ref.topk(2).values
-        if float(top2[0] - top2[1]) >= 0.1:
-            decided += 1
-            decided_ok += same
-    rate = agree / n_check
+    got_all, refs_all = [], []
+    for b, ids in enumerate(prompts):
+        seq = torch.cat([ids, toks[b].long()])
+        for p in range(len(ids) - 1):
+            base.step(int(seq[p]), p)
+        for t in range(n_check):
+            ref = base.step(int(seq[len(ids) - 1 + t]), len(ids) - 1 + t).cpu()
+            refs_all.append(ref)
+            got_all.append(logits[b, t])
+            dd = (logits[b, t] - ref).abs()
+            worst = max(worst, dd.max().item())
+            worst_rms = max(worst_rms, dd.pow(2).mean().sqrt().item())
+            same = int(ref.argmax()) == int(toks[b, t])
+            agree += same
+            if not same and first_div is None:
+                first_div = (b, t)
+            top2 = ref.topk(2).values
+            if float(top2[0] - top2[1]) >= 0.1:
+                decided += 1
+                decided_ok += same
+    n_all = n_check * len(prompts)
+    rate = agree / n_all
     rate_dec = decided_ok / max(decided, 1)
-    floor = overall_agreement_floor(n_check)
-    print(f"validate: {n_check} tokens, teacher-forced greedy agreement {rate * 100:.2f}% (floor {floor * 100:.1f}%) "
-          f"(where the baseline's top-2 gap >= 0.1: {rate_dec * 100:.2f}% of {decided}); "
-          f"first divergence at {first_div}; logits max|d| {worst:.3e}, worst per-step rms {worst_rms:.3e}")
+    floor = overall_agreement_floor(n_all)
+    print(f"validate: {len(prompts)} sequence(s) x {n_check} tokens, teacher-forced greedy agreement "
+          f"{rate * 100:.2f}% (floor {floor * 100:.1f}%) (where the baseline's top-2 gap >= 0.1: "
+          f"{rate_dec * 100:.2f}% of {decided}); first divergence at (sequence, step) {first_div}; "
+          f"logits max|d| {worst:.3e}, worst per-step rms {worst_rms:.3e}")
     # the reference's logit_validation parameters (main.py:51, 542) as restated checks; reported,
     # not part of the pass rule (their rtol on near-zero logits is below the bf16 noise floor)
-    from mk_validate import REFERENCE_DIVERGENCE_TOL, divergences, topk_tolerance
-    tm = topk_tolerance(logits[:n_check], torch.stack(refs))
-    dv = divergences(logits[:n_check], torch.stack(refs), REFERENCE_DIVERGENCE_TOL)
+    got_all, refs_all = torch.stack(got_all), torch.stack(refs_all)
+    tm = topk_tolerance(got_all, refs_all)
+    dv = divergences(got_all, refs_all, REFERENCE_DIVERGENCE_TOL)
     print("validate: reference tol_map (restated; steps passing / worst ratio): " +
           ", ".join(f"{k} {v['steps_passing'] * 100:.1f}% / {v['worst_ratio']:.2f}" for k, v in tm.items()) +
           f"; greedy divergences {dv['steps']}, {dv['within_tol']} within {REFERENCE_DIVERGENCE_TOL}")
@@ -192,24 +255,37 @@ def overall_agreement_floor(n: int) -> float:
     return min(0.90, p - 2.0 * (p * (1.0 - p) / max(n, 1)) ** 0.5)
 
 
+def generate_report(latencies_ms: List[float], tokens: int) -> dict:
+    """Percentiles and throughput of one latency list (the fields of NxDI's
+    generate_report as main.py:178-271 prints them): ``tokens`` is the number
+    of tokens one latency sample covers, batch included."""
+    lat_s = sorted(latencies_ms)
+    pct = lambda q: lat_s[min(len(lat_s) - 1, int(q * len(lat_s)))]
+    return {"latency_ms_p50": pct(0.5), "latency_ms_p90": pct(0.9), "latency_ms_p95": pct(0.95),
+            "latency_ms_p99": pct(0.99), "latency_ms_p100": lat_s[-1], "latency_ms_avg": statistics.mean(lat_s),
+            "throughput": tokens / (statistics.mean(lat_s) / 1e3)}
+
+
 def benchmark_sampling(args):
     """The reference's benchmark_sampling / generate_report (main.py:178-271):
-    e2e, context encoding (prefill) and per-token generation latencies over
-    num_runs runs after one warm-up run. With --graph the token-generation
-    steps of a run replay one captured HIP graph (per-token latency is then
-    the run's generation time / tokens)."""
+    e2e, context encoding (prefill) and per-step token generation latencies
+    over num_runs runs after one warm-up run. With --graph the token-generation
+    steps of a run replay one captured HIP graph (the per-step latency is then
+    the run's generation time / steps)."""
     import mk_lib
-    ids = prompt_ids(args)
-    model = prepare_inference(args)
+    d = tokenizer_dir(args)
+    prompts = encode_prompts(args, load_tokenizer(d) if d else None)
+    B = len(prompts)
+    model = prepare_inference(args, B)
     n_new = args.max_new_tokens
-    sp = sampling_params(args)
+    sp = sampling_params(args, B)
     dec = model.launcher("decode" if sp is None else "decode_logits")
     graph = model.decode_graph(n_new, sampling_params=sp, seed=args.seed) if args.graph else None
     e2e, cte, tkg = [], [], []
     for r in range(args.num_runs + 1):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        model.prefill(ids)
+        model.prefill(prompts)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_new + 1)]
@@ -234,17 +310,17 @@ def benchmark_sampling(args):
             tkg += [ev[0].elapsed_time(ev[n_new]) / n_new] * n_new
         else:
             tkg += [ev[i].elapsed_time(ev[i + 1]) for i in range(n_new)]
-
-    def rep(lat, tokens):
-        lat_s = sorted(lat)
-        pct = lambda q: lat_s[min(len(lat_s) - 1, int(q * len(lat_s)))]
-        return {"latency_ms_p50": pct(0.5), "latency_ms_p90": pct(0.9), "latency_ms_p99": pct(0.99),
-                "latency_ms_avg": statistics.mean(lat), "throughput": tokens / (statistics.mean(lat) / 1e3)}
-    report = {"e2e_model": rep(e2e, len(ids) + n_new),
-              "context_encoding_model": rep(cte, len(ids)),
-              "token_generation_model": rep(tkg, 1)}
+    bits = model.ws.read_device_error() | model.prefill_device_error()
+    if bits:
+        raise RuntimeError(f"megakernel device error bits 0x{bits:x}")
+    n_prompt = sum(int(p.numel()) for p in prompts)
+    report = {"e2e_model": generate_report(e2e, n_prompt + B * n_new),
+              "context_encoding_model": generate_report(cte, n_prompt),
+              "token_generation_model": generate_report(tkg, B),
+              "config": {"batch": B, "prompt_lengths": [int(p.numel()) for p in prompts], "max_new_tokens": n_new,
+                         "graph": bool(args.graph), "num_runs": args.num_runs, "model_path": args.model_path}}
     print(json.dumps(report, indent=4))
-    Path(BENCHMARK_REPORT_FILENAME).write_text(json.dumps(report))
+    Path(args.report_path).write_text(json.dumps(report))
     return report
 
 

@@ -105,10 +105,22 @@ def synthetic_state_dict(seed: int = 0, d: LlamaDims = LLAMA_3_2_1B,
 
 def load_hf_checkpoint(path: str, d: LlamaDims = LLAMA_3_2_1B) -> Dict[str, torch.Tensor]:
     """Read a local HF Llama checkpoint (``*.safetensors``) into the state-dict
-    naming of ``param_specs`` (``model.`` prefix stripped; tied lm_head as in
-    llama.py:1404-1406). Only safetensors is accepted: nothing executable is
-    ever loaded from a checkpoint."""
+    naming of ``param_specs`` (``model.`` prefix stripped). Only safetensors is
+    accepted: nothing executable is ever loaded from a checkpoint.
+
+    The kernel's lm_head is the embedding (tied weights, as Llama-3.2-1B ships
+    and llama.py:1404-1406 ties them when the config asks). A checkpoint whose
+    ``config.json`` sets ``tie_word_embeddings`` to false, or that holds an
+    ``lm_head.weight`` different from ``embed_tokens.weight``, is refused."""
+    import json
     from safetensors.torch import load_file
+
+    cfg_path = os.path.join(path, "config.json")
+    if os.path.exists(cfg_path):
+        with open(cfg_path) as f:
+            cfg = json.load(f)
+        if cfg.get("tie_word_embeddings", True) is False:
+            raise ValueError(f"{path}: tie_word_embeddings is false; the megakernel's lm_head is the embedding")
 
     files = sorted(f for f in os.listdir(path) if f.endswith(".safetensors"))
     if not files:
@@ -125,6 +137,10 @@ def load_hf_checkpoint(path: str, d: LlamaDims = LLAMA_3_2_1B) -> Dict[str, torc
             raise KeyError(f"checkpoint lacks {name}")
         if tuple(sd[name].shape) != shape:
             raise ValueError(f"{name}: shape {tuple(sd[name].shape)} != {shape}")
+    lm = sd.pop("lm_head.weight", None)
+    if lm is not None and not torch.equal(lm.view(torch.int16), sd["embed_tokens.weight"].view(torch.int16)):
+        raise ValueError(f"{path}: lm_head.weight differs from embed_tokens.weight (untied); "
+                         "the megakernel's lm_head is the embedding")
     return sd
 
 

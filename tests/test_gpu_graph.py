@@ -40,7 +40,7 @@ def test_graph_replays_match_eager_steps(sampled):
         graph.replay()
         torch.cuda.synchronize()
         assert m.ws.read_device_error() == 0
-        got = m.graph_tokens.cpu()
+        got = m.graph_tokens[:, 0].cpu()       # [steps, batch]
         say(f"[graph] sampled={sampled} replay {rep}: tokens {got[:6].tolist()}... eager {eager_tokens[:6].tolist()}")
         assert torch.equal(got, eager_tokens)
         assert torch.equal(m.logits[0].cpu(), eager_last)

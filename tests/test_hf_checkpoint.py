@@ -94,3 +94,32 @@ def test_loaded_checkpoint_packs_like_its_source(tmp_path, small):
     for k in a:
         assert torch.equal(a[k].view(torch.int16) if a[k].dtype == torch.bfloat16 else a[k],
                            b[k].view(torch.int16) if b[k].dtype == torch.bfloat16 else b[k]), k
+
+
+def test_untied_lm_head_is_refused(tmp_path, small):
+    """The kernel's lm_head is the embedding: an untied checkpoint would give
+    wrong logits, so it is refused (config flag, or a differing lm_head tensor)."""
+    from safetensors.torch import save_file
+    from mk_weights import load_hf_checkpoint, synthetic_state_dict
+    prod, _ = small
+    m = hf_model(prod, tie=False)
+    m.save_pretrained(tmp_path / "untied", safe_serialization=True)
+    with pytest.raises(ValueError, match="tie_word_embeddings"):
+        load_hf_checkpoint(str(tmp_path / "untied"), prod)
+    # no config.json: the tensors decide
+    sd = synthetic_state_dict(seed=5, d=prod)
+    (tmp_path / "raw").mkdir()
+    other = dict(sd)
+    other["lm_head.weight"] = (sd["embed_tokens.weight"].float() * 2).to(torch.bfloat16)
+    save_file({("" if k == "lm_head.weight" else "model.") + k: v for k, v in other.items()},
+              str(tmp_path / "raw" / "model.safetensors"))
+    with pytest.raises(ValueError, match="untied"):
+        load_hf_checkpoint(str(tmp_path / "raw"), prod)
+    # an lm_head equal to the embedding (a tied checkpoint that stores both) loads, without it
+    (tmp_path / "tied").mkdir()
+    same = dict(sd)
+    same["lm_head.weight"] = sd["embed_tokens.weight"].clone()
+    save_file({("" if k == "lm_head.weight" else "model.") + k: v for k, v in same.items()},
+              str(tmp_path / "tied" / "model.safetensors"))
+    got = load_hf_checkpoint(str(tmp_path / "tied"), prod)
+    assert "lm_head.weight" not in got
