@@ -43,35 +43,47 @@ inline int batch_of_ws_bytes(size_t bytes) {
 }
 
 // Exchange area of a batched step for up to M sequences (bytes), ordinary
-// device memory. Per layer (each part on a 256-byte boundary):
-//   qkv  bf16 [M][3072]   q | fresh k | fresh v of each token
+// device memory. Two kinds of buffers:
+//
+// Written once per launch and read only after an arrival counter is complete
+// (per layer, each part on a 256-byte boundary), through the XCD's L2:
 //   att  bf16 [M16][2048] merged attention output, M16 = M rounded up to 16,
 //                         in MFMA A-tile order (1 KiB per 16 tokens x 32 columns)
 //   h1   bf16 [M][2048]   h + attn
-//   act  bf16 [M16][8192] silu(gate) * up, in the same order
+//   act  bf16 [M16][8192] silu(gate) * up, in A-tile order
 //   h2   bf16 [M][2048]   layer output
-// and, after all layers, the attention partials
+// then, after all layers, the attention partials
 //   part fp32 [layer][M][8 kv][BATT_MAX_SPLIT][m(4) l(4) o(4x64)]
 // and the down-projection partials of the four K quarters
 //   dpart fp32 [layer][4][M][2048].
-// Every buffer is written once per launch and read only after its arrival
-// counter is complete.
+//
+// Sentinel-filled, in two sets that alternate between launches (the epoch
+// picks the set; a launch refills the other one): bytes 0xffff until
+// written, so an attention item polls its own token's q and fresh K/V rows
+// instead of waiting for every workgroup's QKV stores (per layer):
+//   qkv  bf16 [M][3072]   q | fresh k | fresh v of each token
 struct BatchLayout {
-  size_t qkv, att, h1, act, h2, layer;   // within a layer
-  size_t part_base, part_layer, dpart_base, dpart_layer, total;
+  size_t att, h1, act, h2, layer;               // write-once region, within a layer
+  size_t part_base, part_layer, dpart_base, dpart_layer;
+  size_t sq_qkv, sset_layer;                    // sentinel region, within a layer of a set
+  size_t sent_base, sset, total;                // sets at sent_base and sent_base + sset
   static constexpr size_t r256(size_t x) { return (x + 255) / 256 * 256; }
   void init(int M) {
-    qkv = 0;
-    att = r256(qkv + (size_t)M * MK_QKV_ROWS * 2);
-    h1 = r256(att + (size_t)((M + 15) / 16 * 16) * MK_HIDDEN * 2);
+    const size_t M16 = (size_t)(M + 15) / 16 * 16;
+    att = 0;
+    h1 = r256(att + M16 * MK_HIDDEN * 2);
     act = r256(h1 + (size_t)M * MK_HIDDEN * 2);
-    h2 = r256(act + (size_t)((M + 15) / 16 * 16) * MK_INTER * 2);
+    h2 = r256(act + M16 * MK_INTER * 2);
     layer = r256(h2 + (size_t)M * MK_HIDDEN * 2);
     part_base = (size_t)MK_MAX_LAYERS * layer;
     part_layer = r256((size_t)M * MK_N_KV_HEADS * BATT_MAX_SPLIT * 4 * (MK_HEAD_DIM + 2) * 4);
     dpart_base = part_base + (size_t)MK_MAX_LAYERS * part_layer;
     dpart_layer = r256((size_t)DN_KQ * M * MK_HIDDEN * 4);
-    total = dpart_base + (size_t)MK_MAX_LAYERS * dpart_layer;
+    sq_qkv = 0;
+    sset_layer = r256(sq_qkv + (size_t)M * MK_QKV_ROWS * 2);
+    sset = (size_t)MK_MAX_LAYERS * sset_layer;
+    sent_base = r256(dpart_base + (size_t)MK_MAX_LAYERS * dpart_layer);
+    total = sent_base + 2 * sset;
   }
 };
 

@@ -145,8 +145,12 @@ struct BCtx {
   // and whole 16-row tiles per group)
   bool d2;
   int dng, drpg;
+  uint8_t* sset;    // this launch's sentinel-filled exchange set (qkv of every layer)
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
     return reinterpret_cast<uint16_t*>(p->xch + (size_t)li * p->lay.layer + off);
+  }
+  __device__ __forceinline__ uint16_t* sx(int li, size_t off) const {
+    return reinterpret_cast<uint16_t*>(sset + (size_t)li * p->lay.sset_layer + off);
   }
   __device__ __forceinline__ float* part(int li, int b, int h, int sp) const {
     return reinterpret_cast<float*>(p->xch + p->lay.part_base + (size_t)li * p->lay.part_layer) +
@@ -161,6 +165,31 @@ struct BCtx {
 };
 
 __device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
+
+// Integer reductions over the 64 lanes of a wave (every lane gets the result),
+// and an inclusive prefix sum in lane order.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t x = (uint32_t)__shfl_xor((int)v, o, 64);
+    v = x > v ? x : v;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t x = (uint32_t)__shfl_up((int)v, o, 64);
+    if (lane >= o) v += x;
+  }
+  return v;
+}
 
 // ---------------------------------------------------------------------------
 // Hand-overs
@@ -194,6 +223,7 @@ __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho
 __device__ __forceinline__ void wait_grid(const BCtx& c, int li, int k) {
   wait_handover(c.s, c.ho(li, k), c.G / N_SUB, c.G % N_SUB);
 }
+
 // The h2 hand-over: from every workgroup, or with the 2-D down projection from
 // the one workgroup per row group n that sums its K quarters (sub-counter n % 8).
 __device__ __forceinline__ void wait_h2(const BCtx& c, int li) {
@@ -400,7 +430,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
     stage_norm<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, nullptr, R0, R1, L);
   }
   trace_mark(c.s, 2 * xk(li, 1));
-  uint16_t* xq = c.xb(li, p.lay.qkv);
+  uint16_t* xq = c.sx(li, p.lay.sq_qkv);
   for (int tt = 0; tt < ntile; ++tt) {
     f32x4 acc[MT];
 #pragma unroll
@@ -444,7 +474,10 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
     }
     __syncthreads();   // L.red reuse
   }
-  arrive(c.ho(li, HO_QKV), c.w % N_SUB);
+  // decode steps: the attention items poll q and the fresh K/V rows; a prefill
+  // step's attention also reads cache rows other workgroups write in this
+  // launch, so it waits for every workgroup's stores (an arrival counter)
+  if (c.prefill) arrive(c.ho(li, HO_QKV), c.w % N_SUB);
   trace_done(c.s, li, 0);
 }
 
@@ -455,9 +488,17 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
   const BParams& p = *c.p;
   const int lane = lane_id(), t = threadIdx.x;
   const int nitems = L.cum[c.B];
-  const rsrc_t rq = make_rsrc(c.xb(li, p.lay.qkv), (size_t)c.B * QKV_ROWS * 2);
+  const rsrc_t rq = make_rsrc(c.sx(li, p.lay.sq_qkv), (size_t)c.B * QKV_ROWS * 2);
   bool waited = false;
-  for (int it = c.w; it < nitems; it += c.G) {
+  // Round k of the grid takes items [k*G, (k+1)*G): workgroup w takes item k*G + w
+  // in even rounds and k*G + G-1-w in odd ones (zig-zag), so a workgroup's items
+  // come from different parts of the item list. Items are listed (sequence, kv
+  // head, split), so without the zig-zag a workgroup would take the same split
+  // of every head it serves: the last splits, which hold the fresh row and
+  // usually arrive last and merge, would all land on the same workgroups.
+  for (int base = 0, k = 0; base < nitems; base += c.G, ++k) {
+    const int it = base + ((k & 1) ? c.G - 1 - c.w : c.w);
+    if (it >= nitems) continue;
     int b = 0;
     while (L.cum[b + 1] <= it) ++b;
     const int nsb = L.ns[b], rr = it - L.cum[b], h = rr / nsb, sp = rr % nsb;
@@ -472,19 +513,19 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     AttnGroup g0;
     if (!c.prefill) ar.load(0, g0);
     if (wave_id() == 0) {
-      if (!waited) {
-        trace_mark(c.s, 2 * xk(li, 2) - 1);
-        wait_grid(c, li, HO_QKV);
-        trace_mark(c.s, 2 * xk(li, 2));
-      }
+      if (!waited) trace_mark(c.s, 2 * xk(li, 2) - 1);
+      if (!waited && c.prefill) wait_grid(c, li, HO_QKV);
       // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
       const uint32_t base = (uint32_t)b * (QKV_ROWS * 2);
-      const uint32_t off = lane < 32 ? base + (uint32_t)(h * GQA * HD * 2 + lane * 16)
-                         : lane < 40 ? (fresh ? base + (uint32_t)((NQ * HD + h * HD) * 2 + (lane - 32) * 16) : OOB)
-                         : lane < 48 ? (fresh ? base + (uint32_t)((NQ * HD + NKV * HD + h * HD) * 2 + (lane - 40) * 16) : OOB)
-                                     : OOB;
-      const u32x4 v = ld16(rq, off);
-      if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v;
+      uint32_t off[1];
+      off[0] = lane < 32 ? base + (uint32_t)(h * GQA * HD * 2 + lane * 16)
+             : lane < 40 ? (fresh ? base + (uint32_t)((NQ * HD + h * HD) * 2 + (lane - 32) * 16) : OOB)
+             : lane < 48 ? (fresh ? base + (uint32_t)((NQ * HD + NKV * HD + h * HD) * 2 + (lane - 40) * 16) : OOB)
+                         : OOB;
+      u32x4 v[1];
+      poll_bf16<1>(c.s, rq, off, v);   // (complete at once after a prefill step's counter)
+      if (!waited) trace_mark(c.s, 2 * xk(li, 2));
+      if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v[0];
     }
     waited = true;
     __syncthreads();
@@ -768,6 +809,19 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
   trace_done(c.s, li, 4);
 }
 
+// Refill the other sentinel set (the next launch's) with the sentinel: nothing
+// reads it before that launch, and the kernel boundary orders the two.
+// Device-scope stores, so the next launch's polls find them in memory.
+__device__ __forceinline__ void refill_sentinel_set(const BCtx& c, uint32_t epoch) {
+  const BParams& p = *c.p;
+  const rsrc_t r = make_rsrc(p.xch + p.lay.sent_base + (size_t)((epoch + 1u) & 1u) * p.lay.sset, p.lay.sset);
+  int lo, hi;
+  share((int)(p.lay.sset / 16), c.G, c.w, lo, hi);
+  const u32x4 ones = {~0u, ~0u, ~0u, ~0u};
+  for (int i = lo + (int)threadIdx.x; i < hi; i += NT)
+    __builtin_amdgcn_raw_buffer_store_b128(ones, r, (int)((uint32_t)i * 16u), 0, AUX_SC1);
+}
+
 // Order-preserving 64-bit argmax key: larger value first, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
@@ -777,7 +831,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 
 // Final RMSNorm + tied lm_head GEMM (whole tiles per wave) + per-sequence argmax.
 template <int MT>
-__device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
+__device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   const BParams& p = *c.p;
   const int wave = wave_id(), lane = lane_id();
   int V0, V1, R0, R1;
@@ -803,6 +857,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L) {
   wait_h2(c, p.n_layers - 1);
   stage_norm<MT>(c, make_rsrc(c.xb(p.n_layers - 1, p.lay.h2), (size_t)c.B * H * 2), false, p.g_final, R0, R1, L);
   trace_mark(c.s, 2 * xk(p.n_layers, 1));
+  refill_sentinel_set(c, epoch);   // here the stores delay nothing
   f32x4 acc[MT];
   float best[MT][4];
   int bidx[MT][4];
@@ -895,6 +950,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   // (batch 8 measured slower with it: there act is small and the extra hand-over costs more)
   c.d2 = MK_BDOWN_2D && MT == 2 && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
          c.drpg <= RES_MAX;
+  c.sset = p.xch + p.lay.sent_base + (size_t)(epoch & 1u) * p.lay.sset;
   {
     // zero the other counter set for the next launch
     uint32_t* oc = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
@@ -926,7 +982,8 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   if (!run_ok && blockIdx.x == 0 && t == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_PREFILL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   pos_ok = pos_ok && run_ok;
-  if (pos_ok && t == 0) {
+  if (!p.do_lm || !pos_ok) refill_sentinel_set(c, epoch);   // (the lm_head phase refills otherwise)
+  if (pos_ok && wave_id() == 0) {
     // Attention items (sequence, kv head, split of `tr` rows, a multiple of 32).
     // The critical path is the busiest workgroup: about ceil(items / G) items
     // of the longest split. Two plans: about two items per workgroup over all
@@ -934,53 +991,59 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     // item (found by bisection). The second wins ragged batches, where the
     // first's per-sequence rounding leaves some workgroups a third item; with
     // equal lengths the first measured faster, so the second must be clearly
-    // shorter (by 10%) to be chosen.
-    auto plan = [&](long long rr, long long& n_items, long long& longest) {
-      n_items = 0;
-      longest = 0;
-      for (int b = 0; b < c.B; ++b) {
-        const long long n = L.pos[b] + 1;
-        long long ns = (n + rr - 1) / rr;
-        ns = ns < BATT_MAX_SPLIT ? ns : BATT_MAX_SPLIT;
-        const long long rows = ((n + ns - 1) / ns + 31) / 32 * 32;
-        n_items += NKV * ((n + rows - 1) / rows);
-        longest = rows > longest ? rows : longest;
-      }
+    // shorter (by 10%) to be chosen. Lane b of wave 0 plans sequence b, in
+    // 32-bit arithmetic (s_max <= 2^20 and batch <= 32 keep every count below
+    // 2^28): the plan is on the critical path of every step.
+    const int lane = lane_id();
+    const bool on = lane < c.B;
+    const uint32_t n = on ? (uint32_t)L.pos[lane] + 1u : 0u;
+    auto rows_for = [&](uint32_t rr, uint32_t& ns) {
+      ns = (n + rr - 1u) / rr;
+      ns = ns < (uint32_t)BATT_MAX_SPLIT ? ns : (uint32_t)BATT_MAX_SPLIT;
+      return ((n + ns - 1u) / ns + 31u) / 32u * 32u;
     };
-    long long total = 0, maxn = 0;
-    for (int b = 0; b < c.B; ++b) {
-      total += (long long)NKV * (L.pos[b] + 1);
-      maxn = L.pos[b] + 1 > maxn ? L.pos[b] + 1 : maxn;
-    }
-    long long tr = (total + 2LL * c.G - 1) / (2LL * c.G);
-    tr = (tr + 31) / 32 * 32;
-    if (tr < ATT_MIN_ROWS) tr = ATT_MIN_ROWS;
-    long long ia, la, ib, lb;
-    plan(tr, ia, la);
-    long long lo = ATT_MIN_ROWS / 32, hi = (maxn + 31) / 32 > lo ? (maxn + 31) / 32 : lo;   // in units of 32 rows
-    plan(hi * 32, ib, lb);
-    if (ib <= c.G) {
-      while (lo < hi) {
-        const long long mid = (lo + hi) / 2;
-        plan(mid * 32, ib, lb);
-        if (ib <= c.G) hi = mid;
-        else lo = mid + 1;
+    auto plan = [&](uint32_t rr, uint32_t& n_items, uint32_t& longest) {
+      uint32_t ns = 0u, rows = 0u, items = 0u;
+      if (on) {
+        rows = rows_for(rr, ns);
+        items = (uint32_t)NKV * ((n + rows - 1u) / rows);
       }
-      plan(hi * 32, ib, lb);
-      const long long cost_a = (ia + c.G - 1) / c.G * la, cost_b = (ib + c.G - 1) / c.G * lb;
-      if (10 * cost_b < 9 * cost_a) tr = hi * 32;
+      n_items = wave_sum_u32(items);
+      longest = wave_max_u32(rows);
+    };
+    const uint32_t total = wave_sum_u32((uint32_t)NKV * n), maxn = wave_max_u32(n);
+    const uint32_t G2 = 2u * (uint32_t)c.G, Gu = (uint32_t)c.G;
+    uint32_t tr = ((total + G2 - 1u) / G2 + 31u) / 32u * 32u;
+    if (tr < (uint32_t)ATT_MIN_ROWS) tr = ATT_MIN_ROWS;
+    uint32_t ia, la, ib, lb;
+    plan(tr, ia, la);
+    uint32_t lo = ATT_MIN_ROWS / 32, hi = (maxn + 31u) / 32u > lo ? (maxn + 31u) / 32u : lo;   // units of 32 rows
+    plan(hi * 32u, ib, lb);
+    if (ib <= Gu) {
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) / 2u;
+        plan(mid * 32u, ib, lb);
+        if (ib <= Gu) hi = mid;
+        else lo = mid + 1u;
+      }
+      plan(hi * 32u, ib, lb);
+      const unsigned long long cost_a = (unsigned long long)((ia + Gu - 1u) / Gu) * la;
+      const unsigned long long cost_b = (unsigned long long)((ib + Gu - 1u) / Gu) * lb;
+      if (10ull * cost_b < 9ull * cost_a) tr = hi * 32u;
     }
-    L.cum[0] = 0;
-    for (int b = 0; b < c.B; ++b) {
-      const int n = L.pos[b] + 1;
-      int ns = (int)((n + tr - 1) / tr);
-      ns = ns < BATT_MAX_SPLIT ? ns : BATT_MAX_SPLIT;
-      const int rows = ((n + ns - 1) / ns + 31) / 32 * 32;
-      ns = (n + rows - 1) / rows;
-      L.ns[b] = ns;
-      L.rows[b] = rows;
-      L.cum[b + 1] = L.cum[b] + NKV * ns;
+    uint32_t ns = 0u, rows = 0u, items = 0u;
+    if (on) {
+      rows = rows_for(tr, ns);
+      ns = (n + rows - 1u) / rows;
+      items = (uint32_t)NKV * ns;
     }
+    const uint32_t cum = wave_incl_scan_u32(items);   // items of sequences 0..lane
+    if (on) {
+      L.ns[lane] = (int)ns;
+      L.rows[lane] = (int)rows;
+      L.cum[lane + 1] = (int)cum;
+    }
+    if (lane == 0) L.cum[0] = 0;
   }
   __syncthreads();
 
@@ -993,7 +1056,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
       if (c.d2) phase_down2d<MT>(c, li, L);
       else phase_down<MT>(c, li, L);
     }
-    if (p.do_lm) phase_lm<MT>(c, L);
+    if (p.do_lm) phase_lm<MT>(c, L, epoch);
   }
 
   // ---- exit: the last workgroup out publishes the tokens and advances the epoch ----

@@ -1158,9 +1158,15 @@ int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   const size_t n = workspace_bytes / 16;
   hipLaunchKernelGGL(mk_ws_init_kernel, dim3((int)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024)), dim3(256), 0,
                      st, static_cast<u32x4*>(workspace), n, n);
-  if (xe.max_batch == 1)   // batch-1 exchange sets start filled with the sentinel
+  if (xe.max_batch == 1) {   // batch-1 exchange sets start filled with the sentinel
     hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(xe.xch),
                        XCH_BYTES / 16, (size_t)0);
+  } else {                   // so do the two sentinel sets of a batched exchange area
+    BatchLayout lay;
+    lay.init(xe.max_batch);
+    hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st,
+                       reinterpret_cast<u32x4*>(xe.xch + lay.sent_base), 2 * lay.sset / 16, (size_t)0);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MK_ERR_HIP, "workspace init launch: %s", hipGetErrorString(e));
   return MK_OK;

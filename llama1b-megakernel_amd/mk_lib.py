@@ -175,8 +175,8 @@ class Workspace:
             with torch.cuda.device(self.device):
                 check(load().mk_workspace_release(self.buf.data_ptr()))
 
-    def __del__(self):
-        if getattr(self, "_live", False) and not sys.is_finalizing():
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if getattr(self, "_live", False) and not _finalizing():
             try:
                 self.release()
             except Exception:   # never raise from a finaliser
