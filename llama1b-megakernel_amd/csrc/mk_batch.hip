@@ -57,6 +57,9 @@
 #ifndef MK_BDOWN_2D
 #define MK_BDOWN_2D 1
 #endif
+#ifndef MK_BATT_ROUNDS
+#define MK_BATT_ROUNDS 1   // attention ranges per workgroup
+#endif
 
 namespace {
 
@@ -71,7 +74,6 @@ constexpr int RES_MAX = 64;    // residual columns per workgroup kept in LDS (H 
 constexpr int KQ = H / NWAVE;  // 512: the K range of one wave in the split-K phases over H
 constexpr int KS = 16;         // k-steps (of 32 columns) in a weight unit of the LDS-operand phases
 constexpr int DKS = 8;         // k-steps in a unit of the down projection (A operand in registers too)
-constexpr int ATT_MIN_ROWS = 128;
 constexpr int B_MIN_GRID = 32;
 constexpr int C_EXIT = 0, C_ERR = 1, C_EPOCH = 2;   // control words (shared with the batch-1 layout)
 constexpr int HO_QKV = 0, HO_ATT = 1, HO_H1 = 2, HO_ACT = 3, HO_H2 = 4;   // hand-overs of a layer
@@ -126,8 +128,8 @@ struct BLds {
   int pos[BATCH_MAX];
   int tok[BATCH_MAX];
   int ns[BATCH_MAX];
-  int rows[BATCH_MAX];
-  int cum[BATCH_MAX + 1];
+  int ng[BATCH_MAX];         // attention plan: 128-row groups per kv head of each sequence
+  int cum[BATCH_MAX + 1];    // attention plan: first item of each sequence
   int flag;
 };
 
@@ -490,60 +492,61 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
   const int nitems = L.cum[c.B];
   const rsrc_t rq = make_rsrc(c.sx(li, p.lay.sq_qkv), (size_t)c.B * QKV_ROWS * 2);
   bool waited = false;
-  // Round k of the grid takes items [k*G, (k+1)*G): workgroup w takes item k*G + w
-  // in even rounds and k*G + G-1-w in odd ones (zig-zag), so a workgroup's items
-  // come from different parts of the item list. Items are listed (sequence, kv
-  // head, split), so without the zig-zag a workgroup would take the same split
-  // of every head it serves: the last splits, which hold the fresh row and
-  // usually arrive last and merge, would all land on the same workgroups.
-  for (int base = 0, k = 0; base < nitems; base += c.G, ++k) {
-    const int it = base + ((k & 1) ? c.G - 1 - c.w : c.w);
+  // Round k of the grid takes items [k*G, (k+1)*G) (one round unless the grid
+  // is small): workgroup w takes item k*G + w in even rounds and
+  // k*G + G-1-w in odd ones (zig-zag).
+  for (int rbase = 0, k = 0; rbase < nitems; rbase += c.G, ++k) {
+    const int it = rbase + ((k & 1) ? c.G - 1 - c.w : c.w);
     if (it >= nitems) continue;
-    int b = 0;
-    while (L.cum[b + 1] <= it) ++b;
-    const int nsb = L.ns[b], rr = it - L.cum[b], h = rr / nsb, sp = rr % nsb;
-    const int ps = L.pos[b], rows = L.rows[b];
-    const int j0 = sp * rows, j1 = min(j0 + rows, ps + 1);
-    const bool fresh = ps >= j0 && ps < j1;
-    // the item's cached rows do not depend on this step: their first group is issued before the wait for q
-    // (in a prefill step rows of this step's tokens are among them: issued after the wait)
-    const size_t head = (size_t)(c.cache_seq(b) * NKV + h) * p.s_max * HD;
-    AttnRows ar;
-    ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
-    AttnGroup g0;
-    if (!c.prefill) ar.load(0, g0);
-    if (wave_id() == 0) {
-      if (!waited) trace_mark(c.s, 2 * xk(li, 2) - 1);
-      if (!waited && c.prefill) wait_grid(c, li, HO_QKV);
-      // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
-      const uint32_t base = (uint32_t)b * (QKV_ROWS * 2);
-      uint32_t off[1];
-      off[0] = lane < 32 ? base + (uint32_t)(h * GQA * HD * 2 + lane * 16)
-             : lane < 40 ? (fresh ? base + (uint32_t)((NQ * HD + h * HD) * 2 + (lane - 32) * 16) : OOB)
-             : lane < 48 ? (fresh ? base + (uint32_t)((NQ * HD + NKV * HD + h * HD) * 2 + (lane - 40) * 16) : OOB)
-                         : OOB;
-      u32x4 v[1];
-      poll_bf16<1>(c.s, rq, off, v);   // (complete at once after a prefill step's counter)
-      if (!waited) trace_mark(c.s, 2 * xk(li, 2));
-      if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v[0];
-    }
-    waited = true;
-    __syncthreads();
-    if (c.prefill) ar.load(0, g0);
-    attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
-    // publish the partial and count it in; the last arrival merges
-    wait_mem();
-    __syncthreads();
-    if (t == 0) {
-      uint32_t* cp = c.acnt + ((size_t)li * p.max_batch + b) * NKV + h;
-      const uint32_t prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      L.flag = prev == (uint32_t)(nsb - 1);
-    }
-    __syncthreads();
-    if (L.flag) {
-      attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, c.part(li, b, h, 0), nsb, c.xb(li, p.lay.att), b,
-                                                   h * GQA * HD);
-      arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
+    {
+      int b = 0;
+      while (L.cum[b + 1] <= it) ++b;
+      const int nsb = L.ns[b], rr = it - L.cum[b], h = rr / nsb, sp = rr % nsb;
+      const int ngb = L.ng[b];
+      const int ga = sp * ngb / nsb, gb = (sp + 1) * ngb / nsb;   // the piece's groups
+      const int ps = L.pos[b];
+      const int j0 = ga * ATT_GROUP, j1 = min(gb * ATT_GROUP, ps + 1);
+      const bool fresh = ps >= j0 && ps < j1;
+      // the item's cached rows do not depend on this step: their first group is issued before the wait for q
+      // (in a prefill step rows of this step's tokens are among them: issued after the wait)
+      const size_t head = (size_t)(c.cache_seq(b) * NKV + h) * p.s_max * HD;
+      AttnRows ar;
+      ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
+      AttnGroup g0;
+      if (!c.prefill) ar.load(0, g0);
+      if (wave_id() == 0) {
+        if (!waited) trace_mark(c.s, 2 * xk(li, 2) - 1);
+        if (!waited && c.prefill) wait_grid(c, li, HO_QKV);
+        // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
+        const uint32_t base = (uint32_t)b * (QKV_ROWS * 2);
+        uint32_t off[1];
+        off[0] = lane < 32 ? base + (uint32_t)(h * GQA * HD * 2 + lane * 16)
+               : lane < 40 ? (fresh ? base + (uint32_t)((NQ * HD + h * HD) * 2 + (lane - 32) * 16) : OOB)
+               : lane < 48 ? (fresh ? base + (uint32_t)((NQ * HD + NKV * HD + h * HD) * 2 + (lane - 40) * 16) : OOB)
+                           : OOB;
+        u32x4 v[1];
+        poll_bf16<1>(c.s, rq, off, v);   // (complete at once after a prefill step's counter)
+        if (!waited) trace_mark(c.s, 2 * xk(li, 2));
+        if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v[0];
+      }
+      waited = true;
+      __syncthreads();
+      if (c.prefill) ar.load(0, g0);
+      attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
+      // publish the partial and count it in; the last arrival merges
+      wait_mem();
+      __syncthreads();
+      if (t == 0) {
+        uint32_t* cp = c.acnt + ((size_t)li * p.max_batch + b) * NKV + h;
+        const uint32_t prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        L.flag = prev == (uint32_t)(nsb - 1);
+      }
+      __syncthreads();
+      if (L.flag) {
+        attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, c.part(li, b, h, 0), nsb, c.xb(li, p.lay.att), b,
+                                                     h * GQA * HD);
+        arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
+      }
     }
   }
   if (waited) trace_done(c.s, li, 1);
@@ -984,64 +987,39 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   pos_ok = pos_ok && run_ok;
   if (!p.do_lm || !pos_ok) refill_sentinel_set(c, epoch);   // (the lm_head phase refills otherwise)
   if (pos_ok && wave_id() == 0) {
-    // Attention items (sequence, kv head, split of `tr` rows, a multiple of 32).
-    // The critical path is the busiest workgroup: about ceil(items / G) items
-    // of the longest split. Two plans: about two items per workgroup over all
-    // sequences' rows, or the shortest split that keeps every workgroup at one
-    // item (found by bisection). The second wins ragged batches, where the
-    // first's per-sequence rounding leaves some workgroups a third item; with
-    // equal lengths the first measured faster, so the second must be clearly
-    // shorter (by 10%) to be chosen. Lane b of wave 0 plans sequence b, in
+    // Attention work plan. The KV rows of every (sequence, kv head) form a
+    // segment of 128-row groups (an attention item's unit of work: a partial
+    // group costs a full one). Each segment is cut into p_b pieces of whole
+    // groups, as equal as possible; a piece is one item. Every item beyond the
+    // first on a workgroup costs a few us of fixed work (q hand-over, partial
+    // publication, merge), so the plan is the smallest piece size m (in
+    // groups, found by bisection) whose items fit MK_BATT_ROUNDS rounds of the
+    // grid: p_b = ceil(groups_b / m), at most 16 splits per segment. Items are
+    // listed (sequence, kv head, piece). Lane b of wave 0 plans sequence b, in
     // 32-bit arithmetic (s_max <= 2^20 and batch <= 32 keep every count below
-    // 2^28): the plan is on the critical path of every step.
+    // 2^25): the plan is on the critical path of every step.
     const int lane = lane_id();
     const bool on = lane < c.B;
     const uint32_t n = on ? (uint32_t)L.pos[lane] + 1u : 0u;
-    auto rows_for = [&](uint32_t rr, uint32_t& ns) {
-      ns = (n + rr - 1u) / rr;
-      ns = ns < (uint32_t)BATT_MAX_SPLIT ? ns : (uint32_t)BATT_MAX_SPLIT;
-      return ((n + ns - 1u) / ns + 31u) / 32u * 32u;
-    };
-    auto plan = [&](uint32_t rr, uint32_t& n_items, uint32_t& longest) {
-      uint32_t ns = 0u, rows = 0u, items = 0u;
-      if (on) {
-        rows = rows_for(rr, ns);
-        items = (uint32_t)NKV * ((n + rows - 1u) / rows);
-      }
-      n_items = wave_sum_u32(items);
-      longest = wave_max_u32(rows);
-    };
-    const uint32_t total = wave_sum_u32((uint32_t)NKV * n), maxn = wave_max_u32(n);
-    const uint32_t G2 = 2u * (uint32_t)c.G, Gu = (uint32_t)c.G;
-    uint32_t tr = ((total + G2 - 1u) / G2 + 31u) / 32u * 32u;
-    if (tr < (uint32_t)ATT_MIN_ROWS) tr = ATT_MIN_ROWS;
-    uint32_t ia, la, ib, lb;
-    plan(tr, ia, la);
-    uint32_t lo = ATT_MIN_ROWS / 32, hi = (maxn + 31u) / 32u > lo ? (maxn + 31u) / 32u : lo;   // units of 32 rows
-    plan(hi * 32u, ib, lb);
-    if (ib <= Gu) {
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) / 2u;
-        plan(mid * 32u, ib, lb);
-        if (ib <= Gu) hi = mid;
-        else lo = mid + 1u;
-      }
-      plan(hi * 32u, ib, lb);
-      const unsigned long long cost_a = (unsigned long long)((ia + Gu - 1u) / Gu) * la;
-      const unsigned long long cost_b = (unsigned long long)((ib + Gu - 1u) / Gu) * lb;
-      if (10ull * cost_b < 9ull * cost_a) tr = hi * 32u;
+    const uint32_t ng = (n + ATT_GROUP - 1u) / ATT_GROUP;      // 128-row groups per kv head
+    const uint32_t max_ng = wave_max_u32(ng);
+    const uint32_t slots = (uint32_t)MK_BATT_ROUNDS * (uint32_t)c.G;
+    auto pieces = [&](uint32_t m) { return on ? (ng + m - 1u) / m : 0u; };
+    uint32_t lo = (max_ng + BATT_MAX_SPLIT - 1u) / BATT_MAX_SPLIT, hi = max_ng;   // <= 16 splits per segment
+    if (lo < 1u) lo = 1u;
+    if (hi < lo) hi = lo;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2u;
+      if (wave_sum_u32((uint32_t)NKV * pieces(mid)) <= slots) hi = mid;
+      else lo = mid + 1u;
     }
-    uint32_t ns = 0u, rows = 0u, items = 0u;
+    const uint32_t pb = pieces(hi);
+    const uint32_t items = (uint32_t)NKV * pb;
+    const uint32_t incl = wave_incl_scan_u32(items);
     if (on) {
-      rows = rows_for(tr, ns);
-      ns = (n + rows - 1u) / rows;
-      items = (uint32_t)NKV * ns;
-    }
-    const uint32_t cum = wave_incl_scan_u32(items);   // items of sequences 0..lane
-    if (on) {
-      L.ns[lane] = (int)ns;
-      L.rows[lane] = (int)rows;
-      L.cum[lane + 1] = (int)cum;
+      L.ns[lane] = (int)pb;
+      L.ng[lane] = (int)ng;
+      L.cum[lane + 1] = (int)incl;
     }
     if (lane == 0) L.cum[0] = 0;
   }
