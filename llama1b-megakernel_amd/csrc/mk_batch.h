@@ -34,6 +34,15 @@ __host__ __device__ inline size_t bws_cnt_set(int M) {
   return HCNT_BYTES + (size_t)MK_MAX_LAYERS * M * MK_N_KV_HEADS * 4 + (size_t)MK_MAX_LAYERS * DN_MAX * 4;
 }
 __host__ __device__ inline size_t batch_ws_bytes(int M) { return bws_cnt0(M) + 2 * bws_cnt_set(M); }
+// The two counter sets of a batched launch live in a block of uncached device
+// memory owned by the workspace's exchange area (sized for BATCH_MAX, so any
+// block serves any batch), unless built with MK_BCNT_UNCACHED=0, which keeps
+// them in the workspace at bws_cnt0(M).
+#ifndef MK_BCNT_UNCACHED
+#define MK_BCNT_UNCACHED 1
+#endif
+constexpr size_t BCNT_BLOCK_BYTES = 2 * ((size_t)HCNT_BYTES + (size_t)MK_MAX_LAYERS * BATCH_MAX * MK_N_KV_HEADS * 4 +
+                                         (size_t)MK_MAX_LAYERS * DN_MAX * 4);
 // Largest batch a workspace of `bytes` serves with the batched layout (< 2: batch-1 layout).
 inline int batch_of_ws_bytes(size_t bytes) {
   if (bytes < batch_ws_bytes(2)) return 1;
@@ -91,8 +100,9 @@ struct BatchLayout {
 int batch_device_check(int dev, char* msg, size_t msg_len);
 
 // Enqueue one batched step (arguments already validated by mk_decode_step):
-// xch = exchange area of BatchLayout(max_batch).total bytes.
-hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, int max_batch, int grid,
-                        unsigned long long timeout_ticks);
+// xch = exchange area of BatchLayout(max_batch).total bytes, cnt = the two
+// zero-initialised counter sets (2 * bws_cnt_set(max_batch) bytes).
+hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, uint8_t* cnt, int max_batch,
+                        int grid, unsigned long long timeout_ticks);
 
 }  // namespace mk

@@ -51,11 +51,17 @@
 #ifndef MK_BATT_DEPTH
 #define MK_BATT_DEPTH 1
 #endif
+#ifndef MK_BATT_MX
+#define MK_BATT_MX 1       // attention scores on the matrix cores (attn_item_mx)
+#endif
 #ifndef MK_BGU_PRE
 #define MK_BGU_PRE 1
 #endif
 #ifndef MK_BDOWN_2D
 #define MK_BDOWN_2D 1
+#endif
+#ifndef MK_BDOWN_2D_MT1
+#define MK_BDOWN_2D_MT1 0  // the 2-D down projection at batches of up to 16 too
 #endif
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
@@ -66,7 +72,6 @@ namespace {
 using namespace mk;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int XS = H + 8;      // LDS row stride (bf16) of a staged activation matrix (+16 B against bank conflicts)
@@ -77,11 +82,6 @@ constexpr int DKS = 8;         // k-steps in a unit of the down projection (A op
 constexpr int B_MIN_GRID = 32;
 constexpr int C_EXIT = 0, C_ERR = 1, C_EPOCH = 2;   // control words (shared with the batch-1 layout)
 constexpr int HO_QKV = 0, HO_ATT = 1, HO_H1 = 2, HO_ACT = 3, HO_H2 = 4;   // hand-overs of a layer
-
-__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                 0, 0);
-}
 
 struct BParams {
   const uint16_t* w_qkv;
@@ -103,6 +103,7 @@ struct BParams {
   int32_t* next_token;
   uint8_t* ws;
   uint8_t* xch;
+  uint8_t* cnt;         // the two arrival-counter sets
   BatchLayout lay;
   int batch;
   int max_batch;
@@ -507,13 +508,25 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       const int ps = L.pos[b];
       const int j0 = ga * ATT_GROUP, j1 = min(gb * ATT_GROUP, ps + 1);
       const bool fresh = ps >= j0 && ps < j1;
-      // the item's cached rows do not depend on this step: their first group is issued before the wait for q
-      // (in a prefill step rows of this step's tokens are among them: issued after the wait)
+      // the item's cached rows do not depend on this step: its first MK_BATT_DEPTH groups are issued
+      // before the wait for q (in a prefill step rows of this step's tokens are among them: issued after it)
       const size_t head = (size_t)(c.cache_seq(b) * NKV + h) * p.s_max * HD;
       AttnRows ar;
       ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
-      AttnGroup g0;
-      if (!c.prefill) ar.load(0, g0);
+#if MK_BATT_MX
+      AttnGroupMx ring[MK_BATT_DEPTH + 1];
+      auto issue_ahead = [&]() {
+#pragma unroll
+        for (int g = 0; g < MK_BATT_DEPTH; ++g) load_mx(ar, g, ring[g]);
+      };
+#else
+      AttnGroup ring[MK_BATT_DEPTH + 1];
+      auto issue_ahead = [&]() {
+#pragma unroll
+        for (int g = 0; g < MK_BATT_DEPTH; ++g) ar.load(g, ring[g]);
+      };
+#endif
+      if (!c.prefill) issue_ahead();
       if (wave_id() == 0) {
         if (!waited) trace_mark(c.s, 2 * xk(li, 2) - 1);
         if (!waited && c.prefill) wait_grid(c, li, HO_QKV);
@@ -531,8 +544,12 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       }
       waited = true;
       __syncthreads();
-      if (c.prefill) ar.load(0, g0);
-      attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
+      if (c.prefill) issue_ahead();
+#if MK_BATT_MX
+      attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
+#else
+      attn_item<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
+#endif
       // publish the partial and count it in; the last arrival merges
       wait_mem();
       __syncthreads();
@@ -797,15 +814,30 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
   if (L.flag) {
     const rsrc_t rp = make_rsrc(dp, (size_t)DN_KQ * p.max_batch * H * 4);
     uint16_t* h2 = c.xb(li, p.lay.h2);
-    for (int i = t; i < c.B * c.drpg; i += NT) {
-      const int m = i / c.drpg, r = i % c.drpg, row = R0 + r;
-      float sum = 0.f;
+    // four consecutive rows per thread: the four quarters' 16-byte loads are in
+    // flight together (drpg % 16 == 0, so a group never straddles two tokens)
+    const int n4 = c.drpg / 4;
+    for (int i = t; i < c.B * n4; i += NT) {
+      const int m = i / n4, r = (i % n4) * 4, row = R0 + r;
+      u32x4 v[DN_KQ];
 #pragma unroll
-      for (int q = 0; q < DN_KQ; ++q)
-        sum += __uint_as_float(ld_dev4(rp, (uint32_t)((((size_t)q * p.max_batch + m) * H + row) * 4)));
-      const uint32_t hv = f2bf(bf2f(L.res[m][r]) + rbf(sum));
-      st_dev(h2 + (size_t)m * H + row, hv);
-      if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
+      for (int q = 0; q < DN_KQ; ++q) v[q] = ld_dev16(rp, (uint32_t)((((size_t)q * p.max_batch + m) * H + row) * 4));
+      uint32_t hv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < DN_KQ; ++q) sum += __uint_as_float(v[q][j]);
+        hv[j] = f2bf(bf2f(L.res[m][r + j]) + rbf(sum));
+      }
+      const unsigned long long packed = (unsigned long long)(hv[0] | (hv[1] << 16)) |
+                                        ((unsigned long long)(hv[2] | (hv[3] << 16)) << 32);
+      __hip_atomic_store(reinterpret_cast<unsigned long long*>(h2 + (size_t)m * H + row), packed, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (last && p.hidden_out) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p.hidden_out[(size_t)m * H + row + j] = (uint16_t)hv[j];
+      }
     }
     arrive(c.ho(li, HO_H2), n % N_SUB);
   }
@@ -944,14 +976,14 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   const int t = threadIdx.x;
   const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const size_t cset = bws_cnt_set(p.max_batch);
-  uint8_t* cnt0 = p.ws + bws_cnt0(p.max_batch);
+  uint8_t* cnt0 = p.cnt;
   c.hcnt = cnt0 + (size_t)(epoch & 1u) * cset;
   c.acnt = reinterpret_cast<uint32_t*>(c.hcnt + HCNT_BYTES);
   c.dcnt = c.acnt + (size_t)MK_MAX_LAYERS * p.max_batch * NKV;
   c.dng = c.G / DN_KQ;
   c.drpg = c.dng > 0 ? H / c.dng : 0;
   // (batch 8 measured slower with it: there act is small and the extra hand-over costs more)
-  c.d2 = MK_BDOWN_2D && MT == 2 && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
+  c.d2 = MK_BDOWN_2D && (MT == 2 || MK_BDOWN_2D_MT1) && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
          c.drpg <= RES_MAX;
   c.sset = p.xch + p.lay.sent_base + (size_t)(epoch & 1u) * p.lay.sset;
   {
@@ -1105,8 +1137,8 @@ int batch_device_check(int dev, char* msg, size_t msg_len) {
   return d.status;
 }
 
-hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, int max_batch, int grid,
-                        unsigned long long timeout_ticks) {
+hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch, uint8_t* cnt, int max_batch,
+                        int grid, unsigned long long timeout_ticks) {
   BParams kp;
   memset(&kp, 0, sizeof(kp));
   kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
@@ -1137,6 +1169,7 @@ hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch
   kp.next_token = a->next_token;
   kp.ws = static_cast<uint8_t*>(a->workspace);
   kp.xch = xch;
+  kp.cnt = cnt;
   kp.lay.init(max_batch);
   kp.batch = a->batch;
   kp.max_batch = max_batch;

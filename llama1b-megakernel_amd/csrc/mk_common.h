@@ -555,16 +555,18 @@ struct AttnRows {
 // One attention work item: one kv head of one sequence, cached KV rows
 // [j0, jc) plus, if `fresh`, the new row (from LDS), for the 4 q heads of the
 // group (GQA). `rows` describes the head's cache rows (bf16 [s_max][64] for K
-// and for V); `first` holds its first group, already issued with rows.load(0)
-// (the cached rows do not depend on the current step, so a caller issues them
-// before it waits for q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
-// Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
-// of it; rows stream in groups of ATT_GROUP with an online softmax, DEPTH
-// (1 or 2) groups ahead in flight. Writes the item's partial (m[4], l[4],
-// o[4][64]) unnormalised, relative to m.
+// and for V). Rows stream in groups of ATT_GROUP through a ring of DEPTH + 1
+// group buffers, DEPTH groups ahead in flight while one is consumed; group g
+// lives in ring[g % (DEPTH + 1)], and ring[0 .. DEPTH-1] arrive holding groups
+// 0 .. DEPTH-1, already issued with rows.load(g, ring[g]) (the cached rows do
+// not depend on the current step, so a caller issues them before it waits for
+// q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS. Thread t serves
+// row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8.. of it, with an
+// online softmax. Writes the item's partial (m[4], l[4], o[4][64])
+// unnormalised, relative to m.
 template <int DEPTH = 1, int R = ATT_R>
-__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& first, const uint16_t* q_lds,
-                                          bool fresh, float* part, AttnShared& sh) {
+__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R> (&ring)[DEPTH + 1],
+                                          const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
   u32x4 q[GQA];
 #pragma unroll
@@ -670,21 +672,10 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& f
       else consume_full(cur, BoolC<true>());
     }
   };
-  AttnGroupT<R>& A = first;
-  if (DEPTH == 1) {
-    AttnGroupT<R> B;
-    for (int gi = 0; gi < ngroups; gi += 2) {
-      step(gi, A, B);
-      step(gi + 1, B, A);
-    }
-  } else {
-    AttnGroupT<R> B, C;
-    rows.load(1, B);
-    for (int gi = 0; gi < ngroups; gi += 3) {
-      step(gi, A, C);
-      step(gi + 1, B, A);
-      step(gi + 2, C, B);
-    }
+  constexpr int NB = DEPTH + 1;
+  for (int gi = 0; gi < ngroups; gi += NB) {
+#pragma unroll
+    for (int s = 0; s < NB; ++s) step(gi + s, ring[s], ring[(s + DEPTH) % NB]);
   }
   if (fresh) {   // the new row: row-lane 0 of one round
     const bool valid[1] = {rl == 0};
@@ -714,6 +705,221 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& f
       const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
       const float f = m_run[g] == -INFINITY ? 0.f : __expf(m_run[g] - M);
       lv[g] = l_run[g] * f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[g * 8 + e] = acc[g][e] * f;
+    }
+    reduce_stride8<GQA, false>(lv);       // lane: head 2*b5 + b4
+    if ((lane & 15) == 0) sh.sm[wave][lane >> 4] = lv[0];
+    reduce_stride8<GQA * 8, false>(av);   // lane: values 4*(lane >> 3) .. +3 of head-major [4][8]
+    *reinterpret_cast<float4*>(&sh.pv[wave][ch][(lane >> 3) * 4]) = make_float4(av[0], av[1], av[2], av[3]);
+  }
+  lds_sync();
+  {
+    const int g = t >> 6, d = t & 63;
+    float o = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < NWAVE; ++wv) o += sh.pv[wv][d >> 3][g * 8 + (d & 7)];
+    st_dev(part + 2 * GQA + g * HD + d, o);
+    if (t < GQA) {
+      st_dev(part + t, fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t])));
+      st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
+    }
+  }
+  lds_sync();   // LDS reuse by a following item
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// D = A B^T + C over one 16x16x32 bf16 tile (v_mfma_f32_16x16x32_bf16): lane l
+// holds A row l%16 and B row l%16, columns (l/16)*8 .. +7 of the 32; D[i] of
+// lane l is element (row 4*(l/16) + i, column l%16).
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
+// K/V rows of one ATT_GROUP-row group of the MFMA attention item: wave w takes
+// rows 32w .. 32w+31 of the group.
+//   k[t][s]: K as MFMA A operands, 16-row tile t: lane l holds row 32w + 16t + l%16,
+//            dims 32s + (l/16)*8 .. +7
+//   v[r]:    V for the VALU PV product: lane l holds row 32w + 8r + l/8, dims (l%8)*8 .. +7
+// Rows >= jc read zero through out-of-range offsets.
+struct AttnGroupMx {
+  u32x4 k[2][2];
+  u32x4 v[4];
+};
+static_assert(ATT_GROUP == 32 * NWAVE, "a group is 32 rows per wave");
+__device__ __forceinline__ void load_mx(const AttnRows& rows, int gi, AttnGroupMx& g) {
+  const int lane = lane_id(), base = rows.j0 + gi * ATT_GROUP + 32 * wave_id();
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int j = base + 16 * t + (lane & 15);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      g.k[t][s] = ld_stream(rows.rk, j < rows.jc ? (uint32_t)(j * HD + 32 * s + (lane >> 4) * 8) * 2u : OOB);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int j = base + 8 * r + (lane >> 3);
+    g.v[r] = ld_stream(rows.rv, j < rows.jc ? (uint32_t)(j * HD + (lane & 7) * 8) * 2u : OOB);
+  }
+}
+
+// The attention work item of attn_item with the scores on the matrix cores:
+// same inputs, outputs and ring protocol (groups issued with load_mx).
+// Per group and wave, S = K q^T is two 16x16x32 MFMA tiles per 16 rows (rows on
+// M, the 4 q heads on N, q pre-scaled by 1/8, an exact power of two), so lane
+// (q4 = l/16, n = l%16) holds the scores of head n (n < 4; the other columns
+// are padding) for rows 16t + 4*q4 + i. The softmax runs there once per
+// (row, head), against a running maximum shared by the wave; p = exp(s - m)
+// stays fp32 and reaches the VALU PV product (lane: row l/8 of each 8-row
+// round, dims (l%8)*8 ..) through the wave's slice of sh.pv, which the final
+// merge reuses afterwards. The last arrival's merge is that of attn_item.
+template <int DEPTH = 1>
+__device__ __forceinline__ void attn_item_mx(const AttnRows& rows, AttnGroupMx (&ring)[DEPTH + 1],
+                                             const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh) {
+  const int t = threadIdx.x, wave = wave_id(), lane = lane_id(), n = lane & 15, q4 = lane >> 4;
+  // B operands: q of head n (zero for the padding columns), times 1/8
+  u32x4 qb[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (n < GQA) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(q_lds + n * HD + 32 * s + q4 * 8);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+      uint32_t o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = f2bf(bf_lo(w4[e]) * SM_SCALE) | (f2bf(bf_hi(w4[e]) * SM_SCALE) << 16);
+      v = u32x4{o4[0], o4[1], o4[2], o4[3]};
+    }
+    qb[s] = v;
+  }
+  float m_run = -INFINITY, l_part = 0.f;   // head n: the wave's running max, this lane's share of the sum
+  float acc[GQA][8];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  float* pw = &sh.pv[wave][0][0];   // p of the wave's 32 rows: [row][head]
+  const int ngroups = rows.template ngroups<ATT_R>();
+  auto consume = [&](int gi, const AttnGroupMx& gr, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    f32x4 sc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      sc[tt] = mfma16(gr.k[tt][0], qb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc[tt] = mfma16(gr.k[tt][1], qb[1], sc[tt]);
+    }
+    if (MASKED) {
+      const int rb = rows.j0 + gi * ATT_GROUP + 32 * wave + 4 * q4;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (rb + 16 * tt + i >= rows.jc) sc[tt][i] = -INFINITY;
+    }
+    float gm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    gm = max_xor32(max_xor16(gm));   // head n's maximum over the wave's 32 rows
+    const float mn = fmaxf(m_run, gm);
+    const float keep = mn == -INFINITY ? 1.f : __expf(m_run - mn);
+    float p[2][4], ps = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[tt][i] = MASKED && sc[tt][i] == -INFINITY ? 0.f : __expf(sc[tt][i] - mn);
+        ps += p[tt][i];
+      }
+    l_part = fmaf(l_part, keep, ps);
+    m_run = mn;
+    if (n < GQA) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pw[(16 * tt + 4 * q4 + i) * GQA + n] = p[tt][i];
+    }
+    float kg[GQA];
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) kg[g] = lane_val(keep, g);
+    if (kg[0] != 1.f || kg[1] != 1.f || kg[2] != 1.f || kg[3] != 1.f) {
+#pragma unroll
+      for (int g = 0; g < GQA; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= kg[g];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float4 p4 = *reinterpret_cast<const float4*>(pw + (8 * r + (lane >> 3)) * GQA);
+      const float pg[GQA] = {p4.x, p4.y, p4.z, p4.w};
+      const uint32_t w4[4] = {gr.v[r].x, gr.v[r].y, gr.v[r].z, gr.v[r].w};
+#pragma unroll
+      for (int g = 0; g < GQA; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[g][2 * e] = fmaf(pg[g], bf_lo(w4[e]), acc[g][2 * e]);
+          acc[g][2 * e + 1] = fmaf(pg[g], bf_hi(w4[e]), acc[g][2 * e + 1]);
+        }
+    }
+  };
+  auto step = [&](int gi, AttnGroupMx& cur, AttnGroupMx& ahead) {
+    load_mx(rows, gi + DEPTH, ahead);   // past the last group: all rows out of range, nothing read
+    if (gi < ngroups) {
+      if (rows.jc - rows.j0 - gi * ATT_GROUP >= ATT_GROUP) consume(gi, cur, BoolC<false>());
+      else consume(gi, cur, BoolC<true>());
+    }
+  };
+  constexpr int NB = DEPTH + 1;
+  for (int gi = 0; gi < ngroups; gi += NB) {
+#pragma unroll
+    for (int s = 0; s < NB; ++s) step(gi + s, ring[s], ring[(s + DEPTH) % NB]);
+  }
+  wait_mem();   // drain the out-of-range loads issued past the last group
+  // the wave's maximum and sum of head g, in every lane
+  const float l_wave = add_xor32(add_xor16(l_part));
+  float mg[GQA], lg[GQA];
+#pragma unroll
+  for (int g = 0; g < GQA; ++g) {
+    mg[g] = lane_val(m_run, g);
+    lg[g] = lane_val(l_wave, g);
+  }
+  const int ch = t & 7;
+  if (fresh && wave == 0) {   // the new row (from LDS), counted once: wave 0, row-lane 0
+    const u32x4 kf = *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + ch * 8);
+    const u32x4 vf = *reinterpret_cast<const u32x4*>(q_lds + GQA * HD + HD + ch * 8);
+    const uint32_t w4[4] = {vf.x, vf.y, vf.z, vf.w};
+    const bool mine = (lane >> 3) == 0;
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      const u32x4 qv = *reinterpret_cast<const u32x4*>(q_lds + g * HD + ch * 8);
+      const float x = sum_lanes8(dot8(kf, qv, 0.f)) * SM_SCALE;
+      const float mn = fmaxf(mg[g], x);
+      const float keep = mg[g] == -INFINITY ? 1.f : __expf(mg[g] - mn);
+      const float pr = __expf(x - mn);
+      lg[g] = fmaf(lg[g], keep, pr);
+      mg[g] = mn;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[g][2 * e] = fmaf(mine ? pr : 0.f, bf_lo(w4[e]), acc[g][2 * e] * keep);
+        acc[g][2 * e + 1] = fmaf(mine ? pr : 0.f, bf_hi(w4[e]), acc[g][2 * e + 1] * keep);
+      }
+    }
+  }
+  // merge the 8 row-lanes of each wave (lane bits 3-5), then the 4 waves through
+  // LDS (each wave rewrites only its own slice of sh.pv): the wave's max is
+  // uniform, its sum enters once (row-lane 0)
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) sh.mx[wave][g] = mg[g];
+  }
+  lds_sync();
+  {
+    float lv[GQA], av[GQA * 8];
+#pragma unroll
+    for (int g = 0; g < GQA; ++g) {
+      const float M = fmaxf(fmaxf(sh.mx[0][g], sh.mx[1][g]), fmaxf(sh.mx[2][g], sh.mx[3][g]));
+      const float f = mg[g] == -INFINITY ? 0.f : __expf(mg[g] - M);
+      lv[g] = (lane >> 3) == 0 ? lg[g] * f : 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) av[g * 8 + e] = acc[g][e] * f;
     }

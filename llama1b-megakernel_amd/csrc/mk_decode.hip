@@ -454,8 +454,8 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     AttnRows ar;
     ar.init(c.p->kc[li] + (size_t)h * c.p->s_max * HD, c.p->vc[li] + (size_t)h * c.p->s_max * HD, c.p->s_max, j0,
             min(j1, c.pos));
-    AttnGroupT<ATT_RD> g0;
-    ar.load(0, g0);
+    AttnGroupT<ATT_RD> ring[2];
+    ar.load(0, ring[0]);
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2) - 1);
     if (wave_id() == 0) {
       // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
@@ -471,7 +471,7 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     }
     lds_sync();
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2));
-    attn_item(ar, g0, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
+    attn_item<1, ATT_RD>(ar, ring, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
     if (sp == 0)
       attn_merge_head<true, ATT_MAX_SPLIT>(c.s, c.part(li) + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS, nsplit,
                                            c.xb(li, X_ATT) + h * GQA * HD);
@@ -903,11 +903,15 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 //   * batched workspaces (max batch M >= 2): BatchLayout(M).total bytes of
 //     ordinary device memory, whose activation matrices every workgroup reads
 //     through its XCD's L2.
+//     Its arrival counters sit in a BCNT_BLOCK_BYTES block of uncached memory
+//     of the entry (`cnt`): a counter hand-over polled there under a full
+//     weight stream completes sooner than one polled in ordinary memory.
 // A workspace re-initialised with another layout (a new allocation at the
 // same address) gets a matching area; areas it no longer uses stay in the
 // list and are handed to the next workspace that fits. mk_workspace_release
 // returns a workspace's area: an uncached one becomes spare (never freed), an
-// ordinary one is freed and its entry removed.
+// ordinary one is freed and its entry removed, its counter block kept in a
+// spare list for the next batched workspace on the device.
 constexpr size_t XCH_BYTES = 2 * SET_BYTES;
 struct XchEntry {
   const void* ws;   // owner (nullptr: spare)
@@ -915,10 +919,32 @@ struct XchEntry {
   int max_batch;    // 1: batch-1 layout
   size_t bytes;
   uint8_t* xch;
+  uint8_t* cnt;     // batched: uncached counter block (nullptr for batch-1 entries)
 };
 XchEntry g_xch[256];
 int g_n_xch = 0;
+struct CntBlock {
+  int dev;
+  uint8_t* p;
+};
+CntBlock g_cnt_spare[256];   // counter blocks of released batched areas (uncached: never freed)
+int g_n_cnt_spare = 0;
 std::mutex g_xch_mu;
+
+// An uncached counter block for a new batched entry on `dev` (caller holds g_xch_mu).
+int counter_block(int dev, uint8_t** out) {
+  for (int i = 0; i < g_n_cnt_spare; ++i)
+    if (g_cnt_spare[i].dev == dev) {
+      *out = g_cnt_spare[i].p;
+      g_cnt_spare[i] = g_cnt_spare[--g_n_cnt_spare];
+      return MK_OK;
+    }
+  void* p = nullptr;
+  const hipError_t e = hipExtMallocWithFlags(&p, BCNT_BLOCK_BYTES, hipDeviceMallocUncached);
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "counter block allocation: %s", hipGetErrorString(e));
+  *out = static_cast<uint8_t*>(p);
+  return MK_OK;
+}
 
 bool exchange_of(const void* ws, int dev, XchEntry* out) {
   std::lock_guard<std::mutex> lk(g_xch_mu);
@@ -962,10 +988,18 @@ int exchange_create(const void* ws, int dev, int max_batch, XchEntry* out) {
   }
   if (g_n_xch == (int)(sizeof(g_xch) / sizeof(g_xch[0])))
     return fail(MK_ERR_WORKSPACE, "too many workspaces initialised in this process (%d)", g_n_xch);
+  uint8_t* cnt = nullptr;
+  if (!uncached) {
+    const int rc = counter_block(dev, &cnt);
+    if (rc != MK_OK) return rc;
+  }
   void* p = nullptr;
   const hipError_t e = uncached ? hipExtMallocWithFlags(&p, need, hipDeviceMallocUncached) : hipMalloc(&p, need);
-  if (e != hipSuccess) return fail(MK_ERR_HIP, "exchange area allocation (%zu bytes): %s", need, hipGetErrorString(e));
-  g_xch[g_n_xch++] = XchEntry{ws, dev, max_batch, need, static_cast<uint8_t*>(p)};
+  if (e != hipSuccess) {
+    if (cnt) g_cnt_spare[g_n_cnt_spare++] = CntBlock{dev, cnt};
+    return fail(MK_ERR_HIP, "exchange area allocation (%zu bytes): %s", need, hipGetErrorString(e));
+  }
+  g_xch[g_n_xch++] = XchEntry{ws, dev, max_batch, need, static_cast<uint8_t*>(p), cnt};
   *out = g_xch[g_n_xch - 1];
   return MK_OK;
 }
@@ -982,6 +1016,7 @@ int exchange_release(const void* ws, int dev) {
       return MK_OK;
     }
     const hipError_t he = hipFree(e.xch);
+    g_cnt_spare[g_n_cnt_spare++] = CntBlock{dev, e.cnt};
     g_xch[i] = g_xch[--g_n_xch];
     if (he != hipSuccess) return fail(MK_ERR_HIP, "freeing the exchange area: %s", hipGetErrorString(he));
     return MK_OK;
@@ -1166,6 +1201,8 @@ int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
     lay.init(xe.max_batch);
     hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st,
                        reinterpret_cast<u32x4*>(xe.xch + lay.sent_base), 2 * lay.sset / 16, (size_t)0);
+    hipLaunchKernelGGL(mk_ws_init_kernel, dim3(64), dim3(256), 0, st, reinterpret_cast<u32x4*>(xe.cnt),
+                       BCNT_BLOCK_BYTES / 16, BCNT_BLOCK_BYTES / 16);   // counters start at zero
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MK_ERR_HIP, "workspace init launch: %s", hipGetErrorString(e));
@@ -1225,7 +1262,8 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
                   batch_ws_bytes(xe.max_batch));
     const int brc = batch_device_check(dev, g_msg, sizeof(g_msg));
     if (brc != MK_OK) return brc;
-    const hipError_t be = batch_launch(w, a, xe.xch, xe.max_batch, di.grid, di.ticks_per_s * 2ull);
+    uint8_t* cnt = MK_BCNT_UNCACHED ? xe.cnt : static_cast<uint8_t*>(a->workspace) + bws_cnt0(xe.max_batch);
+    const hipError_t be = batch_launch(w, a, xe.xch, cnt, xe.max_batch, di.grid, di.ticks_per_s * 2ull);
     if (be != hipSuccess) return fail(MK_ERR_HIP, "batched kernel launch failed: %s", hipGetErrorString(be));
     return MK_OK;
   }
