@@ -54,6 +54,9 @@
 #ifndef MK_BATT_MX
 #define MK_BATT_MX 1       // attention scores on the matrix cores (attn_item_mx)
 #endif
+#ifndef MK_SPOLL
+#define MK_SPOLL 1         // hand-over counters polled with scalar loads
+#endif
 #ifndef MK_BGU_PRE
 #define MK_BGU_PRE 1
 #endif
@@ -202,7 +205,7 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 // have finished, then one arrival is added to sub-counter `sub` of the hand-over.
 __device__ __forceinline__ void arrive(uint32_t* ho, int sub) {
   wait_mem();
-  __syncthreads();
+  lds_sync();
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ho) + (size_t)sub * CNT_LINE), 1u,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -210,6 +213,34 @@ __device__ __forceinline__ void arrive(uint32_t* ho, int sub) {
 
 // Wait (one full wave) until sub-counter j of a hand-over holds per + (j < extra) arrivals.
 __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho, int per, int extra) {
+#if MK_SPOLL
+  // scalar loads (glc) of the 8 uncached counter lines: the scalar data path
+  // does not queue behind this CU's vector loads in flight
+  // (the halves as unsigned 32-bit values: a signed low half would sign-extend into the high word)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)ho);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uintptr_t)ho >> 32));
+  const unsigned long long base = (unsigned long long)lo | ((unsigned long long)hi << 32);
+  const unsigned long long t0s = wall_clock64();
+  for (int it = 1;; ++it) {
+    uint32_t v0, v1, v2, v3, v4, v5, v6, v7;
+    asm volatile(
+        "s_load_dword %0, %8, 0x0 glc\n\ts_load_dword %1, %8, 0x80 glc\n\t"
+        "s_load_dword %2, %8, 0x100 glc\n\ts_load_dword %3, %8, 0x180 glc\n\t"
+        "s_load_dword %4, %8, 0x200 glc\n\ts_load_dword %5, %8, 0x280 glc\n\t"
+        "s_load_dword %6, %8, 0x300 glc\n\ts_load_dword %7, %8, 0x380 glc\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=s"(v0), "=s"(v1), "=s"(v2), "=s"(v3), "=s"(v4), "=s"(v5), "=s"(v6), "=s"(v7)
+        : "s"(base)
+        : "memory");
+    const uint32_t p0 = (uint32_t)per;
+    const bool ok = v0 >= p0 + (0 < extra) && v1 >= p0 + (1 < extra) && v2 >= p0 + (2 < extra) &&
+                    v3 >= p0 + (3 < extra) && v4 >= p0 + (4 < extra) && v5 >= p0 + (5 < extra) &&
+                    v6 >= p0 + (6 < extra) && v7 >= p0 + (7 < extra);
+    if (ok) return;
+    if (wait_expired(sy, t0s, it)) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#endif
   const int lane = lane_id();
   const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
   const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
@@ -321,37 +352,40 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
   stage_issue<MT>(c, src, gather, L);
   stage_finish<MT, 0>(c, gamma, r0, r1, L);
 }
-template <int MT, int AFTER>
-__device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
-  wait_vm_after<AFTER>();
-  __syncthreads();
-  // RMS per row: 16 threads (a 16-lane row of a wave) per token row, chunk q16 + 16i
-  // (i < 16) of 8 elements each; rows >= B (zeros from the staging) are skipped.
-  // The lanes of a row first copy its raw columns [r0, r1) to L.res (a wave's
-  // LDS accesses complete in order, so before any lane overwrites them), then
-  // read their 16 chunks into registers at once, sum the squares with v_dot2
-  // into two accumulators and write the normalised chunks back from the same
-  // registers: one LDS read and one write per chunk, no branch in the loop.
-  const int q16 = threadIdx.x & 15;
-  for (int m = threadIdx.x >> 4; m < c.B; m += NT / 16) {
+// RMS normalisation of the staged rows in place, TPR threads per token row
+// (16, 32 or 64: the batch's rows spread over all 256 threads), chunk q + TPR*i
+// (i < 256/TPR) of 8 elements each for thread q of its row; rows >= B (zeros
+// from the staging) are skipped. The lanes of a row first copy its raw columns
+// [r0, r1) to L.res (a wave's LDS accesses complete in order, so before any lane
+// overwrites them), then read their chunks into registers at once, sum the
+// squares with v_dot2 into two accumulators and write the normalised chunks
+// back from the same registers: one LDS read and one write per chunk, no branch
+// in the loop.
+template <int MT, int TPR>
+__device__ __forceinline__ void norm_rows(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
+  constexpr int NCH = (H / 8) / TPR;
+  const int q = threadIdx.x & (TPR - 1);
+  for (int m = threadIdx.x / TPR; m < c.B; m += NT / TPR) {
     uint16_t* row = &L.xn[m][0];
-    for (int col = r0 + q16; col < r1; col += 16) L.res[m][col - r0] = row[col];
-    u32x4 x[16];
+    for (int col = r0 + q; col < r1; col += TPR) L.res[m][col - r0] = row[col];
+    u32x4 x[NCH];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = *reinterpret_cast<const u32x4*>(&row[(q16 + 16 * i) * 8]);
+    for (int i = 0; i < NCH; ++i) x[i] = *reinterpret_cast<const u32x4*>(&row[(q + TPR * i) * 8]);
     float ssa = 0.f, ssb = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
+    for (int i = 0; i < NCH; i += 2) {
       ssa = dot8(x[i], x[i], ssa);
       ssb = dot8(x[i + 1], x[i + 1], ssb);
     }
     float ss = ssa + ssb;
     ss = sum_lanes8(ss);
-    ss += dpp<DPP_ROR8>(ss);   // the 16 lanes of the row
+    ss += dpp<DPP_ROR8>(ss);          // the 16 lanes of a DPP row
+    if (TPR >= 32) ss = add_xor16(ss);
+    if (TPR >= 64) ss = add_xor32(ss);
     const float inv = rsqrtf(ss * (1.0f / H) + EPS);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int col = (q16 + 16 * i) * 8;
+    for (int i = 0; i < NCH; ++i) {
+      const int col = (q + TPR * i) * 8;
       uint32_t e[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
       u32x4 gv = {0u, 0u, 0u, 0u};
       if (gamma) gv = *reinterpret_cast<const u32x4*>(gamma + col);
@@ -364,7 +398,15 @@ __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamm
       *reinterpret_cast<u32x4*>(&row[col]) = u32x4{e[0], e[1], e[2], e[3]};
     }
   }
-  __syncthreads();
+}
+template <int MT, int AFTER>
+__device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
+  wait_vm_after<AFTER>();
+  lds_sync();
+  if (c.B <= NT / 64) norm_rows<MT, 64>(c, gamma, r0, r1, L);
+  else if (c.B <= NT / 32) norm_rows<MT, 32>(c, gamma, r0, r1, L);
+  else norm_rows<MT, 16>(c, gamma, r0, r1, L);
+  lds_sync();
 }
 
 // One unit of MFMAs: KS k-steps from column k0, A from the staged LDS matrix.
@@ -395,7 +437,7 @@ __device__ __forceinline__ f32x4 reduce_waves(const f32x4 (&acc)[MT], BLds<MT>& 
   const int wave = wave_id(), lane = lane_id();
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) L.red[wave][mt][lane] = acc[mt];
-  __syncthreads();
+  lds_sync();
   f32x4 d = {0.f, 0.f, 0.f, 0.f};
   if (wave < MT) {
     d = L.red[0][wave][lane];
@@ -475,7 +517,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
         st_dev(xq + (size_t)m * QKV_ROWS + col, outv);
       }
     }
-    __syncthreads();   // L.red reuse
+    lds_sync();   // L.red reuse
   }
   // decode steps: the attention items poll q and the fresh K/V rows; a prefill
   // step's attention also reads cache rows other workgroups write in this
@@ -543,7 +585,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
         if (lane < 48) *reinterpret_cast<u32x4*>(L.q + lane * 8) = v[0];
       }
       waited = true;
-      __syncthreads();
+      lds_sync();
       if (c.prefill) issue_ahead();
 #if MK_BATT_MX
       attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
@@ -552,13 +594,13 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
 #endif
       // publish the partial and count it in; the last arrival merges
       wait_mem();
-      __syncthreads();
+      lds_sync();
       if (t == 0) {
         uint32_t* cp = c.acnt + ((size_t)li * p.max_batch + b) * NKV + h;
         const uint32_t prev = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         L.flag = prev == (uint32_t)(nsb - 1);
       }
-      __syncthreads();
+      lds_sync();
       if (L.flag) {
         attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, c.part(li, b, h, 0), nsb, c.xb(li, p.lay.att), b,
                                                      h * GQA * HD);
@@ -602,7 +644,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
         if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i])));
       }
     }
-    __syncthreads();
+    lds_sync();
   }
   arrive(c.ho(li, HO_H1), c.w % N_SUB);
   trace_done(c.s, li, 2);
@@ -727,7 +769,7 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
           }
         }
       }
-      __syncthreads();
+      lds_sync();
     }
   };
   for (int u = 0; u < nunits; u += 2) {
@@ -795,7 +837,7 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
           if (m < c.B) st_dev(dp + ((size_t)kq * p.max_batch + m) * H + row, d[i]);
         }
       }
-      __syncthreads();
+      lds_sync();
     }
   };
   for (int u = 0; u < nunits; u += 2) {
@@ -804,13 +846,13 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
   }
   // count this quarter in; the row group's last quarter sums the four
   wait_mem();
-  __syncthreads();
+  lds_sync();
   if (t == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(c.dcnt + (size_t)li * DN_MAX + n, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     L.flag = prev == (uint32_t)(DN_KQ - 1);
   }
-  __syncthreads();
+  lds_sync();
   if (L.flag) {
     const rsrc_t rp = make_rsrc(dp, (size_t)DN_KQ * p.max_batch * H * 4);
     uint16_t* h2 = c.xb(li, p.lay.h2);
