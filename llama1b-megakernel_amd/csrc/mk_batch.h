@@ -18,13 +18,17 @@ constexpr int BATT_MAX_SPLIT = 16;  // KV-length splits per (sequence, kv head)
 //   256 + 256*b       u64 argmax key of sequence b (one 256-byte line each)
 //   BWS_CNT0(M) + set*bws_cnt_set(M)     arrival counters of one launch (two sets,
 //                     alternating by epoch; each launch zeroes the other set):
-//     hand-over counters [MK_MAX_LAYERS][5 hand-overs][8 sub-counters], one 128-byte line each
+//     hand-over counters [MK_MAX_LAYERS][5 hand-overs][N_SUB sub-counters], one 128-byte line each
 //     attention-split counters u32 [MK_MAX_LAYERS][M][8 kv heads]
 //     down-projection row-group counters u32 [MK_MAX_LAYERS][DN_MAX]
 constexpr size_t BWS_KEY0 = 256;
 constexpr size_t BWS_KEY_STRIDE = 256;
 constexpr int N_HANDOVER = 5;   // per layer: qkv, att, h1, act, h2
-constexpr int N_SUB = 8;        // sub-counters per hand-over (arrivals spread over 8 lines)
+#ifndef MK_NSUB
+#define MK_NSUB 32   // (8 lines: ~1% slower at batch 8, arrivals to one line serialise)
+#endif
+constexpr int N_SUB = MK_NSUB;  // sub-counters per hand-over (arrivals spread over N_SUB lines)
+static_assert(N_SUB % 8 == 0 && N_SUB <= 64, "8, 16, .. 64 sub-counters");
 constexpr size_t CNT_LINE = 128;
 constexpr size_t HCNT_BYTES = (size_t)MK_MAX_LAYERS * N_HANDOVER * N_SUB * CNT_LINE;
 constexpr int DN_MAX = 256;     // row groups of the 2-D down projection (grid / 4) at most

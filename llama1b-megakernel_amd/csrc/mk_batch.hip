@@ -54,9 +54,6 @@
 #ifndef MK_BATT_MX
 #define MK_BATT_MX 1       // attention scores on the matrix cores (attn_item_mx)
 #endif
-#ifndef MK_SPOLL
-#define MK_SPOLL 1         // hand-over counters polled with scalar loads
-#endif
 #ifndef MK_BGU_PRE
 #define MK_BGU_PRE 1
 #endif
@@ -213,34 +210,6 @@ __device__ __forceinline__ void arrive(uint32_t* ho, int sub) {
 
 // Wait (one full wave) until sub-counter j of a hand-over holds per + (j < extra) arrivals.
 __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho, int per, int extra) {
-#if MK_SPOLL
-  // scalar loads (glc) of the 8 uncached counter lines: the scalar data path
-  // does not queue behind this CU's vector loads in flight
-  // (the halves as unsigned 32-bit values: a signed low half would sign-extend into the high word)
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)ho);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uintptr_t)ho >> 32));
-  const unsigned long long base = (unsigned long long)lo | ((unsigned long long)hi << 32);
-  const unsigned long long t0s = wall_clock64();
-  for (int it = 1;; ++it) {
-    uint32_t v0, v1, v2, v3, v4, v5, v6, v7;
-    asm volatile(
-        "s_load_dword %0, %8, 0x0 glc\n\ts_load_dword %1, %8, 0x80 glc\n\t"
-        "s_load_dword %2, %8, 0x100 glc\n\ts_load_dword %3, %8, 0x180 glc\n\t"
-        "s_load_dword %4, %8, 0x200 glc\n\ts_load_dword %5, %8, 0x280 glc\n\t"
-        "s_load_dword %6, %8, 0x300 glc\n\ts_load_dword %7, %8, 0x380 glc\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=s"(v0), "=s"(v1), "=s"(v2), "=s"(v3), "=s"(v4), "=s"(v5), "=s"(v6), "=s"(v7)
-        : "s"(base)
-        : "memory");
-    const uint32_t p0 = (uint32_t)per;
-    const bool ok = v0 >= p0 + (0 < extra) && v1 >= p0 + (1 < extra) && v2 >= p0 + (2 < extra) &&
-                    v3 >= p0 + (3 < extra) && v4 >= p0 + (4 < extra) && v5 >= p0 + (5 < extra) &&
-                    v6 >= p0 + (6 < extra) && v7 >= p0 + (7 < extra);
-    if (ok) return;
-    if (wait_expired(sy, t0s, it)) return;
-    __builtin_amdgcn_s_sleep(1);
-  }
-#endif
   const int lane = lane_id();
   const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
   const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
@@ -623,8 +592,8 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
   u32x4 wv[KS];
   load_w<KS>(rw, p.tiled, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
   trace_mark(c.s, 2 * xk(li, 3) - 1);
-  // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % 8: B arrivals each
-  wait_handover(c.s, c.ho(li, HO_ATT), c.B, 0);
+  // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % N_SUB
+  wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
   trace_mark(c.s, 2 * xk(li, 3));
   u32x4 a[MT * KS];
   load_a_tiled<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)((c.B + 15) / 16 * 16) * H * 2), c.B, H / 32, wave * KQ, a);
