@@ -531,11 +531,8 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
         for (int g = 0; g < MK_BATT_DEPTH; ++g) load_mx(ar, g, ring[g]);
       };
 #else
-      AttnGroup ring[MK_BATT_DEPTH + 1];
-      auto issue_ahead = [&]() {
-#pragma unroll
-        for (int g = 0; g < MK_BATT_DEPTH; ++g) ar.load(g, ring[g]);
-      };
+      AttnGroup g0;   // (attn_item issues its second group itself at depth 2)
+      auto issue_ahead = [&]() { ar.load(0, g0); };
 #endif
       if (!c.prefill) issue_ahead();
       if (wave_id() == 0) {
@@ -559,7 +556,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
 #if MK_BATT_MX
       attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
 #else
-      attn_item<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
+      attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
 #endif
       // publish the partial and count it in; the last arrival merges
       wait_mem();

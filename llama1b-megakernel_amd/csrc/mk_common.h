@@ -555,18 +555,16 @@ struct AttnRows {
 // One attention work item: one kv head of one sequence, cached KV rows
 // [j0, jc) plus, if `fresh`, the new row (from LDS), for the 4 q heads of the
 // group (GQA). `rows` describes the head's cache rows (bf16 [s_max][64] for K
-// and for V). Rows stream in groups of ATT_GROUP through a ring of DEPTH + 1
-// group buffers, DEPTH groups ahead in flight while one is consumed; group g
-// lives in ring[g % (DEPTH + 1)], and ring[0 .. DEPTH-1] arrive holding groups
-// 0 .. DEPTH-1, already issued with rows.load(g, ring[g]) (the cached rows do
-// not depend on the current step, so a caller issues them before it waits for
-// q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS. Thread t serves
-// row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8.. of it, with an
-// online softmax. Writes the item's partial (m[4], l[4], o[4][64])
-// unnormalised, relative to m.
+// and for V); `first` holds its first group, already issued with rows.load(0)
+// (the cached rows do not depend on the current step, so a caller issues them
+// before it waits for q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
+// Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
+// of it; rows stream in groups of ATT_GROUP with an online softmax, DEPTH
+// (1 or 2) groups ahead in flight. Writes the item's partial (m[4], l[4],
+// o[4][64]) unnormalised, relative to m.
 template <int DEPTH = 1, int R = ATT_R>
-__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R> (&ring)[DEPTH + 1],
-                                          const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh) {
+__device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& first, const uint16_t* q_lds,
+                                          bool fresh, float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
   u32x4 q[GQA];
 #pragma unroll
@@ -672,10 +670,21 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R> (&
       else consume_full(cur, BoolC<true>());
     }
   };
-  constexpr int NB = DEPTH + 1;
-  for (int gi = 0; gi < ngroups; gi += NB) {
-#pragma unroll
-    for (int s = 0; s < NB; ++s) step(gi + s, ring[s], ring[(s + DEPTH) % NB]);
+  AttnGroupT<R>& A = first;
+  if (DEPTH == 1) {
+    AttnGroupT<R> B;
+    for (int gi = 0; gi < ngroups; gi += 2) {
+      step(gi, A, B);
+      step(gi + 1, B, A);
+    }
+  } else {
+    AttnGroupT<R> B, C;
+    rows.load(1, B);
+    for (int gi = 0; gi < ngroups; gi += 3) {
+      step(gi, A, C);
+      step(gi + 1, B, A);
+      step(gi + 2, C, B);
+    }
   }
   if (fresh) {   // the new row: row-lane 0 of one round
     const bool valid[1] = {rl == 0};

@@ -454,8 +454,8 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     AttnRows ar;
     ar.init(c.p->kc[li] + (size_t)h * c.p->s_max * HD, c.p->vc[li] + (size_t)h * c.p->s_max * HD, c.p->s_max, j0,
             min(j1, c.pos));
-    AttnGroupT<ATT_RD> ring[2];
-    ar.load(0, ring[0]);
+    AttnGroupT<ATT_RD> g0;
+    ar.load(0, g0);
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2) - 1);
     if (wave_id() == 0) {
       // q of heads 4h..4h+3 (512 B, lanes 0-31), the fresh K row (lanes 32-39) and V row (40-47)
@@ -471,7 +471,7 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
     }
     lds_sync();
     if (it == c.w) trace_mark(c.s, 2 * xk(li, 2));
-    attn_item<1, ATT_RD>(ar, ring, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
+    attn_item(ar, g0, L.q, fresh, c.part(li) + ((size_t)h * ATT_MAX_SPLIT + sp) * PART_FLOATS, L.att);
     if (sp == 0)
       attn_merge_head<true, ATT_MAX_SPLIT>(c.s, c.part(li) + (size_t)h * ATT_MAX_SPLIT * PART_FLOATS, nsplit,
                                            c.xb(li, X_ATT) + h * GQA * HD);
