@@ -63,6 +63,9 @@
 #ifndef MK_BDOWN_2D_MT1
 #define MK_BDOWN_2D_MT1 0  // the 2-D down projection at batches of up to 16 too
 #endif
+#ifndef MK_BGFIX_256
+#define MK_BGFIX_256 1     // the grid-size-256 instantiations on 256-CU devices
+#endif
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
 #endif
@@ -967,7 +970,9 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   }
 }
 
-template <int MT>
+// GFIX: the grid size when known at compile time (the per-phase work splits
+// then divide by a constant); 0: gridDim.x.
+template <int MT, int GFIX>
 __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   __shared__ BLds<MT> L;
   BCtx c;
@@ -977,7 +982,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.s.timeout = p.timeout_ticks;
   c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
   trace_mark(c.s, 0);
-  c.G = gridDim.x;
+  c.G = GFIX ? GFIX : (int)gridDim.x;
   c.w = blockIdx.x;
   c.B = p.batch;
   c.prefill = (p.flags & MK_FLAG_PREFILL) != 0;
@@ -1114,6 +1119,17 @@ std::mutex g_bdev_mu;
 
 namespace mk {
 
+// The batched kernel for `batch` tokens on a grid of `grid` workgroups: one
+// 16-row MFMA tile up to 16 tokens, two above; MI355X's 256 CUs get the
+// instantiations with the grid size fixed at compile time.
+const void* batch_kernel_for(int batch, int grid) {
+  if (grid == 256 && MK_BGFIX_256)
+    return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 256>)
+                       : reinterpret_cast<const void*>(mk_batch_kernel<2, 256>);
+  return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 0>)
+                     : reinterpret_cast<const void*>(mk_batch_kernel<2, 0>);
+}
+
 int batch_device_check(int dev, char* msg, size_t msg_len) {
   if (dev < 0 || dev >= 64) {
     snprintf(msg, msg_len, "device index %d out of range", dev);
@@ -1126,10 +1142,8 @@ int batch_device_check(int dev, char* msg, size_t msg_len) {
     d.status = MK_OK;
     d.msg[0] = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb1, reinterpret_cast<const void*>(mk_batch_kernel<1>), NT, 0) !=
-            hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb2, reinterpret_cast<const void*>(mk_batch_kernel<2>), NT, 0) !=
-            hipSuccess) {
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb1, batch_kernel_for(1, cus), NT, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb2, batch_kernel_for(17, cus), NT, 0) != hipSuccess) {
       d.status = MK_ERR_HIP;
       snprintf(d.msg, sizeof(d.msg), "device query for the batched kernel failed on device %d", dev);
     } else if (nb1 < 1 || nb2 < 1) {
@@ -1190,8 +1204,7 @@ hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch
   kp.timeout_ticks = timeout_ticks;
   kp.trace = static_cast<unsigned long long*>(a->trace);
   void* args[] = {&kp};
-  const void* fn = a->batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1>)
-                                  : reinterpret_cast<const void*>(mk_batch_kernel<2>);
+  const void* fn = batch_kernel_for(a->batch, grid);
   const hipStream_t st = static_cast<hipStream_t>(a->stream);
   return (a->flags & MK_FLAG_COOPERATIVE) ? hipLaunchCooperativeKernel(fn, dim3(grid), dim3(NT), args, 0, st)
                                           : hipLaunchKernel(fn, dim3(grid), dim3(NT), args, 0, st);

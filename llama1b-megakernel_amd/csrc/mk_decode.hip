@@ -78,6 +78,9 @@ using namespace mk;
 #ifndef MK_ATT_SPLITS
 #define MK_ATT_SPLITS 8
 #endif
+#ifndef MK_GFIX_256
+#define MK_GFIX_256 1      // the grid-size-256 instantiation on 256-CU devices
+#endif
 #ifndef MK_ATT_ROUNDS
 #define MK_ATT_ROUNDS 4
 #endif
@@ -479,6 +482,10 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
   }
 }
 
+// GFIX: the grid size when it is known at compile time (the work splits then
+// divide by a constant: multiply and shift instead of a ~20-instruction
+// division each, ~1.8 us of the prologue at one wave per SIMD); 0: gridDim.x.
+template <int GFIX>
 __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   __shared__ Lds L;
 
@@ -489,7 +496,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   c.s.timeout = p.timeout_ticks;
   c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
   trace_mark(c.s, 0);
-  c.G = gridDim.x;
+  c.G = GFIX ? GFIX : (int)gridDim.x;
   c.w = blockIdx.x;
   // The control words, the position and the token first; then the first
   // layer's QKV weight ring (it depends on nothing), then the loads that need
@@ -866,6 +873,13 @@ struct DeviceInfo {
 DeviceInfo g_dev[64];
 std::mutex g_dev_mu;
 
+// The batch-1 kernel for a grid of `grid` workgroups (one per CU): MI355X's 256
+// CUs get the instantiation with the grid size fixed at compile time.
+const void* decode_kernel_for(int grid) {
+  return grid == 256 && MK_GFIX_256 ? reinterpret_cast<const void*>(mk_decode_kernel<256>)
+                     : reinterpret_cast<const void*>(mk_decode_kernel<0>);
+}
+
 int device_info(int dev, DeviceInfo* out) {
   if (dev < 0 || dev >= 64) return fail(MK_ERR_DEVICE, "device index %d out of range", dev);
   std::lock_guard<std::mutex> lk(g_dev_mu);
@@ -876,10 +890,9 @@ int device_info(int dev, DeviceInfo* out) {
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
         hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
       return fail(MK_ERR_HIP, "hipDeviceGetAttribute failed on device %d", dev);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(mk_decode_kernel), NT, 0) !=
-        hipSuccess)
-      return fail(MK_ERR_HIP, "occupancy query failed");
     d.grid = cus;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel_for(cus), NT, 0) != hipSuccess)
+      return fail(MK_ERR_HIP, "occupancy query failed");
     d.ticks_per_s = (unsigned long long)(clk_khz > 0 ? clk_khz : 100000) * 1000ull;
     d.status = MK_OK;
     if (!coop) d.status = fail(MK_ERR_DEVICE, "device %d lacks cooperative launch", dev);
@@ -1099,11 +1112,10 @@ int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& 
   // kernel is bounded, so a workgroup that is never scheduled shows up as
   // MK_DEVERR_SYNC, not as a hang.
   const hipStream_t st = static_cast<hipStream_t>(a->stream);
-  const hipError_t e =
-      (a->flags & MK_FLAG_COOPERATIVE)
-          ? hipLaunchCooperativeKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args,
-                                       0, st)
-          : hipLaunchKernel(reinterpret_cast<const void*>(mk_decode_kernel), dim3(di.grid), dim3(NT), args, 0, st);
+  const void* fn = decode_kernel_for(di.grid);
+  const hipError_t e = (a->flags & MK_FLAG_COOPERATIVE)
+                           ? hipLaunchCooperativeKernel(fn, dim3(di.grid), dim3(NT), args, 0, st)
+                           : hipLaunchKernel(fn, dim3(di.grid), dim3(NT), args, 0, st);
   if (e != hipSuccess) return fail(MK_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return MK_OK;
 }
