@@ -152,6 +152,8 @@ struct BCtx {
   bool d2;
   int dng, drpg;
   uint8_t* sset;    // this launch's sentinel-filled exchange set (qkv of every layer)
+  uint32_t* cnt_other;   // the other counter set (the next launch's), zeroed by this one
+  int cnt_words;
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
     return reinterpret_cast<uint16_t*>(p->xch + (size_t)li * p->lay.layer + off);
   }
@@ -423,6 +425,69 @@ __device__ __forceinline__ f32x4 reduce_waves(const f32x4 (&acc)[MT], BLds<MT>& 
 // Phases
 // ---------------------------------------------------------------------------
 
+// The work that depends on the positions only: each token's RoPE row (loaded
+// into registers first, written to LDS last, so the loads overlap the plan) and
+// the attention work plan (wave 0). With one MFMA tile it runs while the first
+// layer's weight ring and input staging are in flight.
+template <int MT>
+__device__ __forceinline__ void plan_and_rope(BCtx& c, BLds<MT>& L) {
+  const BParams& p = *c.p;
+  const int t = threadIdx.x;
+  constexpr int RPT = (16 * MT * HD + NT - 1) / NT;   // RoPE words per thread at most
+  uint32_t rv[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = t + k * NT, m = i / HD;
+    rv[k] = 0u;
+    if (i < c.B * HD) {
+      const int ps = L.pos[m];
+      if (ps >= 0 && ps < p.rope_rows) rv[k] = reinterpret_cast<const uint32_t*>(p.rope + (size_t)ps * (2 * HD))[i % HD];
+    }
+  }
+  if (wave_id() == 0) {
+    // Attention work plan. The KV rows of every (sequence, kv head) form a
+    // segment of 128-row groups (an attention item's unit of work: a partial
+    // group costs a full one). Each segment is cut into p_b pieces of whole
+    // groups, as equal as possible; a piece is one item. Every item beyond the
+    // first on a workgroup costs a few us of fixed work (q hand-over, partial
+    // publication, merge), so the plan is the smallest piece size m (in
+    // groups, found by bisection) whose items fit MK_BATT_ROUNDS rounds of the
+    // grid: p_b = ceil(groups_b / m), at most 16 splits per segment. Items are
+    // listed (sequence, kv head, piece). Lane b of wave 0 plans sequence b, in
+    // 32-bit arithmetic (s_max <= 2^20 and batch <= 32 keep every count below
+    // 2^25).
+    const int lane = lane_id();
+    const bool on = lane < c.B;
+    const uint32_t n = on ? (uint32_t)L.pos[lane] + 1u : 0u;
+    const uint32_t ng = (n + ATT_GROUP - 1u) / ATT_GROUP;      // 128-row groups per kv head
+    const uint32_t max_ng = wave_max_u32(ng);
+    const uint32_t slots = (uint32_t)MK_BATT_ROUNDS * (uint32_t)c.G;
+    auto pieces = [&](uint32_t m) { return on ? (ng + m - 1u) / m : 0u; };
+    uint32_t lo = (max_ng + BATT_MAX_SPLIT - 1u) / BATT_MAX_SPLIT, hi = max_ng;   // <= 16 splits per segment
+    if (lo < 1u) lo = 1u;
+    if (hi < lo) hi = lo;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2u;
+      if (wave_sum_u32((uint32_t)NKV * pieces(mid)) <= slots) hi = mid;
+      else lo = mid + 1u;
+    }
+    const uint32_t pb = pieces(hi);
+    const uint32_t items = (uint32_t)NKV * pb;
+    const uint32_t incl = wave_incl_scan_u32(items);
+    if (on) {
+      L.ns[lane] = (int)pb;
+      L.ng[lane] = (int)ng;
+      L.cum[lane + 1] = (int)incl;
+    }
+    if (lane == 0) L.cum[0] = 0;
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = t + k * NT;
+    if (i < c.B * HD) reinterpret_cast<uint32_t*>(L.rope[i / HD])[i % HD] = rv[k];
+  }
+}
+
 // QKV: RMSNorm of the layer input, [Wq;Wk;Wv] GEMM (split-K over the waves),
 // RoPE at each sequence's position; q and the fresh K/V rows to the exchange
 // buffer, K/V also into the caches at row pos[b] of sequence b.
@@ -441,10 +506,11 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
   if (li > 0) {
     wait_h2(c, li - 1);
     stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
-  } else if (p.hidden_in) {
-    stage_norm<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
-  } else {
-    stage_norm<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, nullptr, R0, R1, L);
+  } else {   // the first layer: its input is final data; the plan runs while it lands
+    if (p.hidden_in) stage_issue<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, L);
+    else stage_issue<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, L);
+    if (MT == 1) plan_and_rope<MT>(c, L);   // (two tiles: in the prologue; inlined here it spills)
+    stage_finish<MT, 0>(c, nullptr, R0, R1, L);
   }
   trace_mark(c.s, 2 * xk(li, 1));
   uint16_t* xq = c.sx(li, p.lay.sq_qkv);
@@ -571,8 +637,12 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       }
       lds_sync();
       if (L.flag) {
-        attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, c.part(li, b, h, 0), nsb, c.xb(li, p.lay.att), b,
-                                                     h * GQA * HD);
+        // (instantiated for the segment's split count: every slot up to MAXS is a load)
+        float* ph = c.part(li, b, h, 0);
+        uint16_t* att = c.xb(li, p.lay.att);
+        if (nsb <= 4) attn_merge_head<false, 4, true>(c.s, ph, nsb, att, b, h * GQA * HD);
+        else if (nsb <= 8) attn_merge_head<false, 8, true>(c.s, ph, nsb, att, b, h * GQA * HD);
+        else attn_merge_head<false, BATT_MAX_SPLIT, true>(c.s, ph, nsb, att, b, h * GQA * HD);
         arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
       }
     }
@@ -868,6 +938,17 @@ __device__ __forceinline__ void refill_sentinel_set(const BCtx& c, uint32_t epoc
     __builtin_amdgcn_raw_buffer_store_b128(ones, r, (int)((uint32_t)i * 16u), 0, AUX_SC1);
 }
 
+// Zero the other counter set (the next launch's) and refill its sentinel set:
+// nothing in this launch uses either, so this runs where the stores delay no
+// load (behind the lm_head stream, or after the last layer).
+__device__ __forceinline__ void prepare_next_launch(const BCtx& c, uint32_t epoch) {
+  refill_sentinel_set(c, epoch);
+  int lo, hi;
+  share(c.cnt_words, c.G, c.w, lo, hi);
+  for (int i = lo + (int)threadIdx.x; i < hi; i += NT)
+    __hip_atomic_store(c.cnt_other + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Order-preserving 64-bit argmax key: larger value first, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
@@ -903,7 +984,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   wait_h2(c, p.n_layers - 1);
   stage_norm<MT>(c, make_rsrc(c.xb(p.n_layers - 1, p.lay.h2), (size_t)c.B * H * 2), false, p.g_final, R0, R1, L);
   trace_mark(c.s, 2 * xk(p.n_layers, 1));
-  refill_sentinel_set(c, epoch);   // here the stores delay nothing
+  prepare_next_launch(c, epoch);   // here the stores delay nothing
   f32x4 acc[MT];
   float best[MT][4];
   int bidx[MT][4];
@@ -999,26 +1080,14 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.d2 = MK_BDOWN_2D && (MT == 2 || MK_BDOWN_2D_MT1) && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
          c.drpg <= RES_MAX;
   c.sset = p.xch + p.lay.sent_base + (size_t)(epoch & 1u) * p.lay.sset;
-  {
-    // zero the other counter set for the next launch
-    uint32_t* oc = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
-    int lo, hi;
-    share((int)(cset / 4), c.G, c.w, lo, hi);
-    for (int i = lo + t; i < hi; i += NT) __hip_atomic_store(oc + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  c.cnt_other = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
+  c.cnt_words = (int)(cset / 4);
   if (t < c.B) {
     L.pos[t] = p.pos[t];
     const int tok = p.tokens ? p.tokens[t] : 0;
     L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
   }
   __syncthreads();
-  // each token's RoPE row (read once; positions beyond the table are refused below)
-  for (int i = t; i < c.B * HD; i += NT) {
-    const int m = i / HD, ps = L.pos[m];
-    if (ps >= 0 && ps < p.rope_rows)
-      reinterpret_cast<uint32_t*>(L.rope[m])[i % HD] =
-          reinterpret_cast<const uint32_t*>(p.rope + (size_t)ps * (2 * HD))[i % HD];
-  }
   bool pos_ok = true, run_ok = true;
   for (int b = 0; b < c.B; ++b) {
     const int ps = L.pos[b];
@@ -1030,45 +1099,10 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   if (!run_ok && blockIdx.x == 0 && t == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_PREFILL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   pos_ok = pos_ok && run_ok;
-  if (!p.do_lm || !pos_ok) refill_sentinel_set(c, epoch);   // (the lm_head phase refills otherwise)
-  if (pos_ok && wave_id() == 0) {
-    // Attention work plan. The KV rows of every (sequence, kv head) form a
-    // segment of 128-row groups (an attention item's unit of work: a partial
-    // group costs a full one). Each segment is cut into p_b pieces of whole
-    // groups, as equal as possible; a piece is one item. Every item beyond the
-    // first on a workgroup costs a few us of fixed work (q hand-over, partial
-    // publication, merge), so the plan is the smallest piece size m (in
-    // groups, found by bisection) whose items fit MK_BATT_ROUNDS rounds of the
-    // grid: p_b = ceil(groups_b / m), at most 16 splits per segment. Items are
-    // listed (sequence, kv head, piece). Lane b of wave 0 plans sequence b, in
-    // 32-bit arithmetic (s_max <= 2^20 and batch <= 32 keep every count below
-    // 2^25): the plan is on the critical path of every step.
-    const int lane = lane_id();
-    const bool on = lane < c.B;
-    const uint32_t n = on ? (uint32_t)L.pos[lane] + 1u : 0u;
-    const uint32_t ng = (n + ATT_GROUP - 1u) / ATT_GROUP;      // 128-row groups per kv head
-    const uint32_t max_ng = wave_max_u32(ng);
-    const uint32_t slots = (uint32_t)MK_BATT_ROUNDS * (uint32_t)c.G;
-    auto pieces = [&](uint32_t m) { return on ? (ng + m - 1u) / m : 0u; };
-    uint32_t lo = (max_ng + BATT_MAX_SPLIT - 1u) / BATT_MAX_SPLIT, hi = max_ng;   // <= 16 splits per segment
-    if (lo < 1u) lo = 1u;
-    if (hi < lo) hi = lo;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) / 2u;
-      if (wave_sum_u32((uint32_t)NKV * pieces(mid)) <= slots) hi = mid;
-      else lo = mid + 1u;
-    }
-    const uint32_t pb = pieces(hi);
-    const uint32_t items = (uint32_t)NKV * pb;
-    const uint32_t incl = wave_incl_scan_u32(items);
-    if (on) {
-      L.ns[lane] = (int)pb;
-      L.ng[lane] = (int)ng;
-      L.cum[lane + 1] = (int)incl;
-    }
-    if (lane == 0) L.cum[0] = 0;
+  if (MT == 2 && pos_ok) {
+    plan_and_rope<MT>(c, L);
+    lds_sync();
   }
-  __syncthreads();
 
   if (pos_ok) {
     for (int li = 0; li < p.n_layers; ++li) {
@@ -1081,6 +1115,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     }
     if (p.do_lm) phase_lm<MT>(c, L, epoch);
   }
+  if (!p.do_lm || !pos_ok) prepare_next_launch(c, epoch);   // (the lm_head phase does it otherwise)
 
   // ---- exit: the last workgroup out publishes the tokens and advances the epoch ----
   trace_mark(c.s, MK_TRACE_SLOTS - 1);
