@@ -580,8 +580,10 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
     const int it = rbase + ((k & 1) ? c.G - 1 - c.w : c.w);
     if (it >= nitems) continue;
     {
-      int b = 0;
-      while (L.cum[b + 1] <= it) ++b;
+      // the item's sequence: the number of sequences whose items all come
+      // before it (cum is non-decreasing; one LDS read per lane and a ballot)
+      const int lane_b = lane < c.B ? L.cum[lane + 1] : 0x7fffffff;
+      const int b = __popcll(__ballot(lane_b <= it));
       const int nsb = L.ns[b], rr = it - L.cum[b], h = rr / nsb, sp = rr % nsb;
       const int ngb = L.ng[b];
       const int ga = sp * ngb / nsb, gb = (sp + 1) * ngb / nsb;   // the piece's groups
