@@ -1090,11 +1090,14 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
   }
   __syncthreads();
-  bool pos_ok = true, run_ok = true;
-  for (int b = 0; b < c.B; ++b) {
-    const int ps = L.pos[b];
-    pos_ok = pos_ok && ps >= 0 && ps < p.s_max && ps < p.rope_rows;
-    run_ok = run_ok && (!c.prefill || ps == L.pos[0] + b);
+  // every sequence's position in range (and consecutive in a prefill step):
+  // lane b checks sequence b, each wave the whole batch
+  bool pos_ok, run_ok;
+  {
+    const int lane = lane_id();
+    const int ps = lane < c.B ? L.pos[lane] : 0;
+    pos_ok = __ballot(lane < c.B && !(ps >= 0 && ps < p.s_max && ps < p.rope_rows)) == 0ull;
+    run_ok = __ballot(lane < c.B && c.prefill && ps != L.pos[0] + lane) == 0ull;
   }
   if (!pos_ok && blockIdx.x == 0 && t == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1128,19 +1131,20 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     L.flag = prev == (uint32_t)(c.G - 1);
   }
   __syncthreads();
-  if (!L.flag || t != 0) return;
-  ctrl[C_EXIT] = 0u;
-  ctrl[C_EPOCH] = epoch + 1u;
-  if (pos_ok) {
-    for (int b = 0; b < c.B; ++b) {
-      if (p.do_lm) {
-        unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + BWS_KEY0 + (size_t)b * BWS_KEY_STRIDE);
-        const unsigned long long key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *kp = 0ull;
-        if (p.next_token) p.next_token[b] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
-      }
-      if (p.flags & MK_FLAG_ADVANCE) p.pos[b] = L.pos[b] + 1;
+  if (!L.flag) return;
+  if (t == 0) {
+    ctrl[C_EXIT] = 0u;
+    ctrl[C_EPOCH] = epoch + 1u;
+  }
+  if (pos_ok && t < c.B) {   // thread b: sequence b (one memory round trip, not B in a row)
+    const int b = t;
+    if (p.do_lm) {
+      unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + BWS_KEY0 + (size_t)b * BWS_KEY_STRIDE);
+      const unsigned long long key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *kp = 0ull;
+      if (p.next_token) p.next_token[b] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
     }
+    if (p.flags & MK_FLAG_ADVANCE) p.pos[b] = L.pos[b] + 1;
   }
 }
 
