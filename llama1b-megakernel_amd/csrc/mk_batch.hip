@@ -175,28 +175,38 @@ struct BCtx {
 __device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
 
 // Integer reductions over the 64 lanes of a wave (every lane gets the result),
-// and an inclusive prefix sum in lane order.
+// and an inclusive prefix sum in lane order: DPP steps within each 16-lane row,
+// then the four row results through v_readlane (a lane shuffle would be an LDS
+// round trip per step).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;   // row_shr:n (0 shifted in)
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
-  return v;
+  v += dpp_u32<DPP_XOR1>(v);
+  v += dpp_u32<DPP_XOR2>(v);
+  v += dpp_u32<DPP_ROR4>(v);
+  v += dpp_u32<DPP_ROR8>(v);   // every lane: the sum of its row
+  return (lane_u32(v, 0) + lane_u32(v, 16)) + (lane_u32(v, 32) + lane_u32(v, 48));
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t x = (uint32_t)__shfl_xor((int)v, o, 64);
-    v = x > v ? x : v;
-  }
-  return v;
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, dpp_u32<DPP_XOR1>(v));
+  v = mx(v, dpp_u32<DPP_XOR2>(v));
+  v = mx(v, dpp_u32<DPP_ROR4>(v));
+  v = mx(v, dpp_u32<DPP_ROR8>(v));
+  return mx(mx(lane_u32(v, 0), lane_u32(v, 16)), mx(lane_u32(v, 32), lane_u32(v, 48)));
 }
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
   const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t x = (uint32_t)__shfl_up((int)v, o, 64);
-    if (lane >= o) v += x;
-  }
-  return v;
+  v += dpp_u32<DPP_SHR1>(v);
+  v += dpp_u32<DPP_SHR2>(v);
+  v += dpp_u32<DPP_SHR4>(v);
+  v += dpp_u32<DPP_SHR8>(v);   // inclusive scan within each row
+  const uint32_t r0 = lane_u32(v, 15), r1 = lane_u32(v, 31), r2 = lane_u32(v, 47);
+  return v + (lane >= 16 ? r0 : 0u) + (lane >= 32 ? r1 : 0u) + (lane >= 48 ? r2 : 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -951,6 +961,26 @@ __device__ __forceinline__ void prepare_next_launch(const BCtx& c, uint32_t epoc
     __hip_atomic_store(c.cnt_other + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Maximum of a 64-bit value over each 16-lane DPP row, in every lane of the
+// row: quad swaps, then rotations by 4 and 8 within the row (both halves moved
+// by the same DPP control; no LDS round trip as a lane shuffle would take).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long max_row16_u64(unsigned long long k) {
+  unsigned long long o = dpp_u64<DPP_XOR1>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<DPP_XOR2>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<DPP_ROR4>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<DPP_ROR8>(k);
+  return o > k ? o : k;
+}
+
 // Order-preserving 64-bit argmax key: larger value first, then lower index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
@@ -1034,11 +1064,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       unsigned long long k = bidx[mt][i] == 0x7fffffff ? 0ull : argmax_key(best[mt][i], bidx[mt][i]);
-#pragma unroll
-      for (int sh = 8; sh >= 1; sh >>= 1) {
-        const unsigned long long o = __shfl_xor(k, sh, 64);
-        k = o > k ? o : k;
-      }
+      k = max_row16_u64(k);
       if ((lane & 15) == 0) L.key[wave][mt * 16 + (lane >> 4) * 4 + i] = k;
     }
   __syncthreads();
