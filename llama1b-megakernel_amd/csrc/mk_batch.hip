@@ -345,16 +345,20 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
 // squares with v_dot2 into two accumulators and write the normalised chunks
 // back from the same registers: one LDS read and one write per chunk, no branch
 // in the loop.
-template <int MT, int TPR>
+template <int MT, int TPR, bool GAMMA>
 __device__ __forceinline__ void norm_rows(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
   constexpr int NCH = (H / 8) / TPR;
   const int q = threadIdx.x & (TPR - 1);
   for (int m = threadIdx.x / TPR; m < c.B; m += NT / TPR) {
     uint16_t* row = &L.xn[m][0];
     for (int col = r0 + q; col < r1; col += TPR) L.res[m][col - r0] = row[col];
-    u32x4 x[NCH];
+    u32x4 x[NCH], gvs[GAMMA ? NCH : 1];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) x[i] = *reinterpret_cast<const u32x4*>(&row[(q + TPR * i) * 8]);
+    if (GAMMA) {   // every chunk's gamma issued at once (one memory round trip for the row)
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) gvs[i] = *reinterpret_cast<const u32x4*>(gamma + (q + TPR * i) * 8);
+    }
     float ssa = 0.f, ssb = 0.f;
 #pragma unroll
     for (int i = 0; i < NCH; i += 2) {
@@ -372,12 +376,12 @@ __device__ __forceinline__ void norm_rows(const BCtx& c, const uint16_t* gamma, 
       const int col = (q + TPR * i) * 8;
       uint32_t e[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
       u32x4 gv = {0u, 0u, 0u, 0u};
-      if (gamma) gv = *reinterpret_cast<const u32x4*>(gamma + col);
+      if (GAMMA) gv = gvs[i];
       const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const uint32_t n = cvt_bf2(bf_lo(e[k]) * inv, bf_hi(e[k]) * inv);
-        e[k] = gamma ? cvt_bf2(bf_lo(g[k]) * bf_lo(n), bf_hi(g[k]) * bf_hi(n)) : n;
+        e[k] = GAMMA ? cvt_bf2(bf_lo(g[k]) * bf_lo(n), bf_hi(g[k]) * bf_hi(n)) : n;
       }
       *reinterpret_cast<u32x4*>(&row[col]) = u32x4{e[0], e[1], e[2], e[3]};
     }
@@ -387,9 +391,15 @@ template <int MT, int AFTER>
 __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
   wait_vm_after<AFTER>();
   lds_sync();
-  if (c.B <= NT / 64) norm_rows<MT, 64>(c, gamma, r0, r1, L);
-  else if (c.B <= NT / 32) norm_rows<MT, 32>(c, gamma, r0, r1, L);
-  else norm_rows<MT, 16>(c, gamma, r0, r1, L);
+  if (gamma) {   // the final norm (once per step)
+    if (c.B <= NT / 64) norm_rows<MT, 64, true>(c, gamma, r0, r1, L);
+    else if (c.B <= NT / 32) norm_rows<MT, 32, true>(c, gamma, r0, r1, L);
+    else norm_rows<MT, 16, true>(c, gamma, r0, r1, L);
+  } else {
+    if (c.B <= NT / 64) norm_rows<MT, 64, false>(c, gamma, r0, r1, L);
+    else if (c.B <= NT / 32) norm_rows<MT, 32, false>(c, gamma, r0, r1, L);
+    else norm_rows<MT, 16, false>(c, gamma, r0, r1, L);
+  }
   lds_sync();
 }
 
