@@ -66,6 +66,9 @@
 #ifndef MK_BGFIX_256
 #define MK_BGFIX_256 1     // the grid-size-256 instantiations on 256-CU devices
 #endif
+#ifndef MK_BLM_ODD
+#define MK_BLM_ODD 91      // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
+#endif
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
 #endif
@@ -1006,8 +1009,10 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   int V0, V1, R0, R1;
   // vocabulary rows in multiples of 8: in the tiled lm_head the 8 rows of a
   // lane group are one 128-byte run of each block (a share of 501 rows would
-  // split most 16-row tiles between two workgroups at odd offsets)
-  share(VOCAB / 8, c.G, c.w, V0, V1);
+  // split most 16-row tiles between two workgroups at odd offsets). Workgroup
+  // w runs on XCD w % 8, and the odd XCDs stream this phase ~5% slower than
+  // the even ones on average: the odd-numbered workgroups get fewer rows.
+  share_parity(VOCAB / 8, c.G, c.w, 100, MK_BLM_ODD, V0, V1);
   V0 *= 8;
   V1 *= 8;
   share(H, c.G, c.w, R0, R1);

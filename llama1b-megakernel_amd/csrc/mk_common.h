@@ -340,6 +340,20 @@ __device__ __forceinline__ void share(int total, int n, int i, int& lo, int& hi)
   }
 }
 
+// Share [lo, hi) of `total` items for part i of n, even-numbered parts
+// weighing `a` and odd-numbered ones `b` (a, b in 1..100).
+__device__ __forceinline__ void share_parity(int total, int n, int i, int a, int b, int& lo, int& hi) {
+  auto wsum = [&](int k) { return (uint32_t)(((k + 1) >> 1) * a + (k >> 1) * b); };
+  const uint32_t s = wsum(n);
+  if ((unsigned long long)(unsigned)total * s <= 0xffffffffull) {
+    lo = (int)((uint32_t)total * wsum(i) / s);
+    hi = (int)((uint32_t)total * wsum(i + 1) / s);
+  } else {
+    lo = (int)((unsigned long long)total * wsum(i) / s);
+    hi = (int)((unsigned long long)total * wsum(i + 1) / s);
+  }
+}
+
 // Sentinel tests. bf16 exchange data: any 16-bit lane equal to 0xffff.
 // fp32 exchange data: a whole word equal to 0xffffffff.
 __device__ __forceinline__ bool sent_bf16(uint32_t w) { return (w | 0xffff0000u) == 0xffffffffu || w >= 0xffff0000u; }

@@ -115,6 +115,11 @@ static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
 #endif
 constexpr int D_EARLY = MK_D_EARLY;
 static_assert(D_EARLY >= 0 && D_EARLY <= 16, "down-projection early chunks");
+// lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
+#ifndef MK_LM_ODD
+#define MK_LM_ODD 100
+#endif
+static_assert(MK_LM_ODD > 0 && MK_LM_ODD <= 100, "lm_head parity weight");
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -760,7 +765,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     // ---- final norm + tied lm_head + argmax ----
     if (p.do_lm) {
       int V0, V1;
-      share(VOCAB, G, w, V0, V1);
+      share_parity(VOCAB, G, w, 100, MK_LM_ODD, V0, V1);
       RowStream<8, 4> ls;
       const Span sp = wave_span(V0, V1);
       ls.start(make_rsrc(p.embed, EMBED_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
