@@ -648,7 +648,15 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       lds_sync();
       if (c.prefill) issue_ahead();
 #if MK_BATT_MX
-      attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att);
+      // the head's only split writes the final output, no partial (with two
+      // MFMA tiles, where every head has one split at long contexts)
+      const bool only = MT == 2 && nsb == 1;
+      attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att,
+                                  only ? c.xb(li, p.lay.att) : nullptr, b, h * GQA * HD);
+      if (only) {
+        arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
+        continue;
+      }
 #else
       attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
 #endif

@@ -505,6 +505,15 @@ __device__ __forceinline__ float dot2048(const u32x4 (&wv)[4], const u32x4 (&xs)
   return a + b;
 }
 
+// Element offset of (row m, column j) in a bf16 matrix kept in MFMA A-tile
+// order with kblocks = columns / 32: the 1 KiB block (m / 16, j / 32), 16-byte
+// slot ((j % 32) / 8) * 16 + m % 16 (the lane of v_mfma_f32_16x16x32_bf16 that
+// takes it), element j % 8.
+__device__ __forceinline__ size_t a_tile_off(int m, int j, int kblocks) {
+  return ((size_t)(m >> 4) * (size_t)kblocks + (size_t)(j >> 5)) * 512 +
+         (size_t)((((j & 31) >> 3) << 4) + (m & 15)) * 8 + (size_t)(j & 7);
+}
+
 struct AttnShared {
   float mx[NWAVE][GQA];
   float sm[NWAVE][GQA];
@@ -798,9 +807,15 @@ __device__ __forceinline__ void load_mx(const AttnRows& rows, int gi, AttnGroupM
 // stays fp32 and reaches the VALU PV product (lane: row l/8 of each 8-row
 // round, dims (l%8)*8 ..) through the wave's slice of sh.pv, which the final
 // merge reuses afterwards. The last arrival's merge is that of attn_item.
+//
+// att (optional): the item is the head's only split, and it writes the final
+// output o / l (the value the merge of its one partial would give, bit for
+// bit) as bf16 to row tok, columns col0 .. of a [tokens][2048] matrix in A-tile
+// order instead of the partial.
 template <int DEPTH = 1>
 __device__ __forceinline__ void attn_item_mx(const AttnRows& rows, AttnGroupMx (&ring)[DEPTH + 1],
-                                             const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh) {
+                                             const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh,
+                                             uint16_t* att = nullptr, int tok = 0, int col0 = 0) {
   const int t = threadIdx.x, wave = wave_id(), lane = lane_id(), n = lane & 15, q4 = lane >> 4;
   // B operands: q of head n (zero for the padding columns), times 1/8
   u32x4 qb[2];
@@ -957,10 +972,17 @@ __device__ __forceinline__ void attn_item_mx(const AttnRows& rows, AttnGroupMx (
     float o = 0.f;
 #pragma unroll
     for (int wv = 0; wv < NWAVE; ++wv) o += sh.pv[wv][d >> 3][g * 8 + (d & 7)];
-    st_dev(part + 2 * GQA + g * HD + d, o);
-    if (t < GQA) {
-      st_dev(part + t, fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t])));
-      st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
+    if (att) {
+      const uint32_t mine = f2bf(o / (sh.sm[0][g] + sh.sm[1][g] + sh.sm[2][g] + sh.sm[3][g]));
+      const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine, DPP_XOR1, 0xf, 0xf, false);
+      if ((d & 1) == 0)
+        st_dev(reinterpret_cast<uint32_t*>(att + a_tile_off(tok, col0 + g * HD + d, 2048 / 32)), mine | (next << 16));
+    } else {
+      st_dev(part + 2 * GQA + g * HD + d, o);
+      if (t < GQA) {
+        st_dev(part + t, fmaxf(fmaxf(sh.mx[0][t], sh.mx[1][t]), fmaxf(sh.mx[2][t], sh.mx[3][t])));
+        st_dev(part + GQA + t, sh.sm[0][t] + sh.sm[1][t] + sh.sm[2][t] + sh.sm[3][t]);
+      }
     }
   }
   lds_sync();   // LDS reuse by a following item
@@ -983,15 +1005,6 @@ __device__ __forceinline__ void attn_split(int n_rows, int max_split, int min_ro
 // the caller knows they are complete and they are read once (device scope).
 // MAXS: the most splits a call may pass.
 constexpr int ATT_MERGE_MAX = 8;   // splits the polled merge reads at most
-
-// Element offset of (row m, column j) in a bf16 matrix kept in MFMA A-tile
-// order with kblocks = columns / 32: the 1 KiB block (m / 16, j / 32), 16-byte
-// slot ((j % 32) / 8) * 16 + m % 16 (the lane of v_mfma_f32_16x16x32_bf16 that
-// takes it), element j % 8.
-__device__ __forceinline__ size_t a_tile_off(int m, int j, int kblocks) {
-  return ((size_t)(m >> 4) * (size_t)kblocks + (size_t)(j >> 5)) * 512 +
-         (size_t)((((j & 31) >> 3) << 4) + (m & 15)) * 8 + (size_t)(j & 7);
-}
 
 // TILED: att is the base of a [tokens][2048] matrix in A-tile order and the
 // head's 256 outputs go to row tok, columns col0 ..; otherwise att points at
