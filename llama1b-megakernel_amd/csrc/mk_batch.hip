@@ -67,7 +67,7 @@
 #define MK_BGFIX_256 1     // the grid-size-256 instantiations on 256-CU devices
 #endif
 #ifndef MK_BLM_ODD
-#define MK_BLM_ODD 91      // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
+#define MK_BLM_ODD 100     // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
 #endif
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
@@ -1018,8 +1018,8 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   // vocabulary rows in multiples of 8: in the tiled lm_head the 8 rows of a
   // lane group are one 128-byte run of each block (a share of 501 rows would
   // split most 16-row tiles between two workgroups at odd offsets). Workgroup
-  // w runs on XCD w % 8, and the odd XCDs stream this phase ~5% slower than
-  // the even ones on average: the odd-numbered workgroups get fewer rows.
+  // w runs on XCD w % 8; MK_BLM_ODD < 100 gives the odd-numbered ones (the odd
+  // XCDs) fewer rows.
   share_parity(VOCAB / 8, c.G, c.w, 100, MK_BLM_ODD, V0, V1);
   V0 *= 8;
   V1 *= 8;
