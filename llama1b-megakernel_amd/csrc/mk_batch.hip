@@ -514,8 +514,21 @@ __device__ __forceinline__ void plan_and_rope(BCtx& c, BLds<MT>& L) {
 // QKV: RMSNorm of the layer input, [Wq;Wk;Wv] GEMM (split-K over the waves),
 // RoPE at each sequence's position; q and the fresh K/V rows to the exchange
 // buffer, K/V also into the caches at row pos[b] of sequence b.
+// The first tile's weight unit of the QKV phase of run-layer li (issued by
+// the caller: for the first layer at kernel start, before anything waits).
 template <int MT>
-__device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
+__device__ __forceinline__ void qkv_first_unit(const BCtx& c, int li, u32x4 (&wv)[KS]) {
+  const BParams& p = *c.p;
+  int P0, P1;
+  share(QKV_PAIRS, c.G, c.w, P0, P1);
+  const int row0 = 2 * P0, row_end = 2 * P1;
+  const rsrc_t rw = make_rsrc(p.w_qkv + (size_t)(p.first_layer + li) * QKV_ROWS * H, QKV_LAYER_BYTES);
+  load_w<KS>(rw, p.tiled, row_end > row0 ? row0 : row_end, row_end, H * 2, wave_id() * KQ, wv);
+}
+// FIRST: the first layer (its weight unit already issued, its input final
+// data); the others issue their unit here and wait for the previous layer's h2.
+template <int MT, bool FIRST>
+__device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L, u32x4 (&wv)[KS]) {
   const BParams& p = *c.p;
   const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
   int P0, P1, R0, R1;
@@ -523,10 +536,9 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L) {
   share(H, c.G, c.w, R0, R1);
   const int row0 = 2 * P0, row_end = 2 * P1, ntile = (row_end - row0 + 15) / 16;
   const rsrc_t rw = make_rsrc(p.w_qkv + (size_t)l * QKV_ROWS * H, QKV_LAYER_BYTES);
-  u32x4 wv[KS];
-  load_w<KS>(rw, p.tiled, ntile > 0 ? row0 : row_end, row_end, H * 2, wave * KQ, wv);
+  if (!FIRST) qkv_first_unit<MT>(c, li, wv);
   trace_mark(c.s, 2 * xk(li, 1) - 1);
-  if (li > 0) {
+  if (!FIRST) {
     wait_h2(c, li - 1);
     stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
   } else {   // the first layer: its input is final data; the plan runs while it lands
@@ -1120,6 +1132,16 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.prefill = (p.flags & MK_FLAG_PREFILL) != 0;
   const int t = threadIdx.x;
   const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int tok = 0, ps = 0;
+  if (t < c.B) {
+    ps = p.pos[t];
+    tok = p.tokens ? p.tokens[t] : 0;
+  }
+  // the first layer's first QKV weight unit depends on nothing: issued behind
+  // the control, position and token loads, so that the setup below and the
+  // plan run while it lands
+  u32x4 wv[KS];
+  qkv_first_unit<MT>(c, 0, wv);
   const size_t cset = bws_cnt_set(p.max_batch);
   uint8_t* cnt0 = p.cnt;
   c.hcnt = cnt0 + (size_t)(epoch & 1u) * cset;
@@ -1134,11 +1156,10 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.cnt_other = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
   c.cnt_words = (int)(cset / 4);
   if (t < c.B) {
-    L.pos[t] = p.pos[t];
-    const int tok = p.tokens ? p.tokens[t] : 0;
+    L.pos[t] = ps;
     L.tok[t] = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
   }
-  __syncthreads();
+  lds_sync();   // (not __syncthreads: that would also wait for the weight unit)
   // every sequence's position in range (and consecutive in a prefill step):
   // lane b checks sequence b, each wave the whole batch
   bool pos_ok, run_ok;
@@ -1159,13 +1180,17 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   }
 
   if (pos_ok) {
+    phase_qkv<MT, true>(c, 0, L, wv);
     for (int li = 0; li < p.n_layers; ++li) {
-      phase_qkv<MT>(c, li, L);
       phase_attn<MT>(c, li, L);
       phase_o<MT>(c, li, L);
       phase_gu<MT>(c, li, L);
       if (c.d2) phase_down2d<MT>(c, li, L);
       else phase_down<MT>(c, li, L);
+      if (li + 1 < p.n_layers) {
+        u32x4 wn[KS];
+        phase_qkv<MT, false>(c, li + 1, L, wn);
+      }
     }
     if (p.do_lm) phase_lm<MT>(c, L, epoch);
   }
