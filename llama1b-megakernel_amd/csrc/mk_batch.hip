@@ -1038,9 +1038,21 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   share(H, c.G, c.w, R0, R1);
   const int ntile = (V1 - V0 + 15) / 16;
   constexpr int UPT = H / (KS * 32);
+  static_assert(UPT % 2 == 0, "unit pairs stay within a tile");
   const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
   const int nunits = my_tiles * UPT;
+  // every wave runs the same number of units (rounds of NWAVE tiles; a wave
+  // without a tile in the last round streams nothing), so the rounds' LDS
+  // barriers match
+  const int all_units = (ntile + NWAVE - 1) / NWAVE * UPT;
   const rsrc_t rw = make_rsrc(p.lm, EMBED_BYTES);
+  // the logits of a round: each wave's tile goes to LDS (the split-K area, idle
+  // here), then every thread stores 32 contiguous bytes of one token's 64 rows,
+  // so a token's logits leave in 256-byte runs instead of 64-byte pieces
+  static_assert(sizeof(L.red) == (size_t)16 * MT * 64 * 4, "logit staging area");
+  float (*stage)[64] = reinterpret_cast<float (*)[64]>(&L.red[0][0][0]);
+  const rsrc_t rlog = make_rsrc(p.logits ? (const void*)p.logits : (const void*)p.lm,
+                                p.logits ? (size_t)c.B * VOCAB * 4 : 0);
   auto issue = [&](int u, u32x4(&wv)[KS]) {
     load_w<KS>(rw, p.tiled, u < nunits ? V0 + 16 * (wave + NWAVE * (u / UPT)) : V1, V1, H * 2, (u % UPT) * KS * 32, wv);
   };
@@ -1071,27 +1083,39 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
     issue(u + 2, wv);
     if (u % UPT == UPT - 1) {
       const int row = V0 + 16 * (wave + NWAVE * (u / UPT)) + (lane & 15);
-      if (row < V1) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = mt * 16 + (lane >> 4) * 4 + i;
-            const float v = acc[mt][i];
-            if (m < c.B) {
-              if (p.logits) p.logits[(size_t)m * VOCAB + row] = v;
-              if (v > best[mt][i]) {   // a lane's rows ascend: keeps the lowest index among equal maxima
-                best[mt][i] = v;
-                bidx[mt][i] = row;
-              }
-            }
+        for (int i = 0; i < 4; ++i) {
+          const int m = mt * 16 + (lane >> 4) * 4 + i;
+          const float v = acc[mt][i];
+          stage[m][wave * 16 + (lane & 15)] = v;
+          if (row < V1 && m < c.B && v > best[mt][i]) {   // a lane's rows ascend: keeps the lowest index among equal maxima
+            best[mt][i] = v;
+            bidx[mt][i] = row;
           }
+        }
+      lds_sync();
+      {   // thread t: token t / 8, rows 8*(t % 8) .. +7 of the round
+        const int t = threadIdx.x, m = t >> 3, r8 = (t & 7) * 8;
+        const int row0 = V0 + 16 * NWAVE * (u / UPT) + r8;   // (V0, V1 and rows multiples of 8)
+        const bool ok = m < c.B && row0 < V1;
+        const uint32_t off = ok ? ((uint32_t)m * (uint32_t)VOCAB + (uint32_t)row0) * 4u : OOB;
+        const float4 a = *reinterpret_cast<const float4*>(&stage[m < 16 * MT ? m : 0][r8]);
+        const float4 b = *reinterpret_cast<const float4*>(&stage[m < 16 * MT ? m : 0][r8 + 4]);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(a.x), __float_as_uint(a.y), __float_as_uint(a.z),
+                                                     __float_as_uint(a.w)},
+                                               rlog, (int)off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(b.x), __float_as_uint(b.y), __float_as_uint(b.z),
+                                                     __float_as_uint(b.w)},
+                                               rlog, (int)(ok ? off + 16u : OOB), 0, 0);
       }
+      lds_sync();   // the stage is rewritten in the next round
     }
   };
-  for (int u = 0; u < nunits; u += 2) {
+  for (int u = 0; u < all_units; u += 2) {
     unit(u, wa);
-    if (u + 1 < nunits) unit(u + 1, wb);
+    unit(u + 1, wb);
   }
   // best per token over the 16 lanes of each lane row, then over the waves
 #pragma unroll
