@@ -72,6 +72,12 @@
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
 #endif
+#ifndef MK_BGU_LDS
+#define MK_BGU_LDS 1       // one tile: the last gate/up weight unit copied to LDS during the h1 wait
+#endif
+#ifndef MK_BGU_CH
+#define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
+#endif
 
 namespace {
 
@@ -138,6 +144,14 @@ struct BLds {
   int ng[BATCH_MAX];         // attention plan: 128-row groups per kv head of each sequence
   int cum[BATCH_MAX + 1];    // attention plan: first item of each sequence
   int flag;
+  // gate/up with one token tile: the last weight unit of each wave's tile,
+  // copied from HBM while the workgroup waits for h1 (k-step s of wave w at
+  // gw[(w*KS + s)*64], lane l's 16 bytes at + l, the register unit's lane
+  // order), and a 1 KiB area per wave that copies past it write (two tiles
+  // leave no room in LDS for either)
+  static constexpr int GW = MT == 1 && MK_BGU_LDS ? NWAVE * KS * 64 : 1;
+  u32x4 gw[GW];
+  u32x4 gspare[GW > 1 ? NWAVE * 64 : 1];
 };
 
 struct BCtx {
@@ -240,6 +254,74 @@ __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho
     __builtin_amdgcn_s_sleep(1);
   }
 }
+// One weight unit (KS k-steps in load_w's lane layout) copied from HBM into
+// LDS at dst (KS x 1 KiB: k-step s at dst + s*64, lane l's 16 bytes at + l), a
+// few 1 KiB copies at a time, so that the copies fill the hand-over wait
+// before the unit is used without one burst of them queueing ahead of the
+// poll.
+struct UnitCopy {
+  rsrc_t r;
+  uint32_t o, step;
+  int next;   // k-steps issued (KS: all, or no copy)
+  __device__ __forceinline__ void init(rsrc_t rw, bool tiled, int row, int row_end, uint32_t row_bytes, int k0,
+                                       bool on) {
+    const int lane = lane_id();
+    const int n = row + (lane & 15);
+    if (tiled) {
+      const uint32_t kb = row_bytes / 64u;
+      o = (((uint32_t)n >> 4) * kb + ((uint32_t)k0 >> 5)) * 1024u + (uint32_t)(lane >> 4) * 256u + (uint32_t)(n & 15) * 16u;
+      step = 1024u;
+    } else {
+      o = (uint32_t)n * row_bytes + (uint32_t)(k0 + (lane >> 4) * 8) * 2u;
+      step = 64u;
+    }
+    if (n >= row_end) o = OOB;
+    r = rw;
+    next = on ? 0 : KS;
+  }
+  // up to n more k-steps
+  __device__ __forceinline__ void issue(int n, u32x4* dst) {
+    const int end = min(KS, next + n);
+    for (; next < end; ++next)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(dst + next * 64), 16, o + (uint32_t)next * step, 0, 0,
+                                               AUX_NT);
+  }
+  // the rest, as exactly K copy instructions (a fixed count, so that a wait
+  // for loads issued before them can count past them): k-steps already issued
+  // go to `spare`, a 1 KiB area nobody reads, from an out-of-range offset
+  // (no memory read)
+  template <int K>
+  __device__ __forceinline__ void issue_fixed(u32x4* dst, u32x4* spare) {
+    const int nx = __builtin_amdgcn_readfirstlane(next);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int ck = nx + k;
+      const bool real = ck < KS;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(real ? dst + ck * 64 : spare), 16,
+                                               real ? o + (uint32_t)ck * step : OOB, 0, 0, AUX_NT);
+    }
+    next = min(KS, nx + K);
+  }
+};
+
+// wait_handover that issues `ch` more copies of `uc` after every poll that
+// finds the hand-over incomplete (the next poll queues behind them).
+__device__ __forceinline__ void wait_handover_copy(const Sync& sy, const uint32_t* ho, int per, int extra,
+                                                   UnitCopy& uc, int ch, u32x4* dst) {
+  const int lane = lane_id();
+  const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
+  const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
+  const uint32_t target = lane < N_SUB ? (uint32_t)(per + (lane < extra ? 1 : 0)) : 0u;
+  const unsigned long long t0 = wall_clock64();
+  for (int it = 1;; ++it) {
+    const uint32_t v = ld_dev4(r, off);
+    if (__all(v >= target)) return;
+    if (wait_expired(sy, t0, it)) return;
+    uc.issue(ch, dst);
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // A hand-over produced by every workgroup of the grid (workgroup w adds to sub-counter w % 8).
 __device__ __forceinline__ void wait_grid(const BCtx& c, int li, int k) {
   wait_handover(c.s, c.ho(li, k), c.G / N_SUB, c.G % N_SUB);
@@ -752,28 +834,39 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
                (u % UPT) * KS * 32, wv);
   };
   u32x4 wa[KS], wb[KS];
+  // With one token tile, a wave with one weight tile takes that tile's last
+  // unit from an LDS copy made during the h1 wait (HBM is mostly idle then);
+  // the copies the wait leaves are issued behind the staging.
+  constexpr bool GL = BLds<MT>::GW > 1;
+  static_assert(UPT == 4, "gate/up unit schedule");
+  const bool gl = GL && nunits == UPT;
+  UnitCopy uc;
+  if (GL) uc.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (UPT - 1) * KS * 32, gl);
+  u32x4* gdst = &L.gw[GL ? wave * KS * 64 : 0];
   // MK_BGU_PRE weight units are issued before the h1 wait, the others right
   // behind the h1 staging copies, so the staging does not queue behind them
   if (MK_BGU_PRE >= 1) issue(0, wa);
   if (MK_BGU_PRE >= 2) issue(1, wb);
   trace_mark(c.s, 2 * xk(li, 4) - 1);
-  wait_grid(c, li, HO_H1);
+  if (GL) wait_handover_copy(c.s, c.ho(li, HO_H1), c.G / N_SUB, c.G % N_SUB, uc, MK_BGU_CH, gdst);
+  else wait_grid(c, li, HO_H1);
   stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L);
   if (MK_BGU_PRE < 1) issue(0, wa);
   if (MK_BGU_PRE < 2) issue(1, wb);
+  if (GL) uc.issue_fixed<KS>(gdst, &L.gspare[GL ? wave * 64 : 0]);
   // the raw columns kept for the down projection's residual: its rows
   const int D0 = c.d2 ? (c.w / DN_KQ) * c.drpg : R0, D1 = c.d2 ? D0 + c.drpg : R1;
-  stage_finish<MT, (2 - MK_BGU_PRE) * KS>(c, nullptr, D0, D1, L);
+  stage_finish<MT, (2 - MK_BGU_PRE) * KS + (GL ? KS : 0)>(c, nullptr, D0, D1, L);
   trace_mark(c.s, 2 * xk(li, 4));
   uint16_t* act = c.xb(li, p.lay.act);
   f32x4 acc[MT];
-  auto unit = [&](int u, u32x4(&wv)[KS]) {
+  auto unit = [&](int u, u32x4(&wv)[KS], bool refill) {
     if (u % UPT == 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     mma_lds<MT>(L, (u % UPT) * KS * 32, wv, acc);
-    issue(u + 2, wv);
+    if (refill) issue(u + 2, wv);
     if (u % UPT == UPT - 1) {
       const int row = row0 + 16 * (wave + NWAVE * (u / UPT)) + (lane & 15);
       const bool gate = (row & 1) == 0;
@@ -789,9 +882,19 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
         }
     }
   };
-  for (int u = 0; u < nunits; u += 2) {
-    unit(u, wa);
-    if (u + 1 < nunits) unit(u + 1, wb);
+  if (gl) {   // units 0-2 from registers (unit 2 issued after unit 0), unit 3 from LDS
+    unit(0, wa, true);
+    unit(1, wb, false);
+    unit(2, wa, false);
+    wait_mem();   // the copies were issued before unit 2's loads
+#pragma unroll
+    for (int s = 0; s < KS; ++s) wa[s] = gdst[s * 64 + lane];
+    unit(3, wa, false);
+  } else {
+    for (int u = 0; u < nunits; u += 2) {
+      unit(u, wa, true);
+      if (u + 1 < nunits) unit(u + 1, wb, true);
+    }
   }
   arrive(c.ho(li, HO_ACT), c.w % N_SUB);
   trace_done(c.s, li, 3);
