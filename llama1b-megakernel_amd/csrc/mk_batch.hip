@@ -78,6 +78,15 @@
 #ifndef MK_BGU_CH
 #define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
 #endif
+#ifndef MK_BDN_PAIR
+#define MK_BDN_PAIR 1      // 8-row down shares: each operand load carries two k-steps
+#endif
+#ifndef MK_BDN_RING
+#define MK_BDN_RING 4      // its weight/act units in flight per wave
+#endif
+#ifndef MK_BDN_PRE
+#define MK_BDN_PRE 4       // of which issued before the act wait (weights only)
+#endif
 
 namespace {
 
@@ -168,6 +177,7 @@ struct BCtx {
   // and whole 16-row tiles per group)
   bool d2;
   int dng, drpg;
+  bool dpair;       // every workgroup has at most 8 rows of the (1-D) down projection
   uint8_t* sset;    // this launch's sentinel-filled exchange set (qkv of every layer)
   uint32_t* cnt_other;   // the other counter set (the next launch's), zeroed by this one
   int cnt_words;
@@ -967,6 +977,107 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
   trace_done(c.s, li, 4);
 }
 
+// The down projection of a workgroup with at most 8 rows (a 256-workgroup
+// grid) at batches of at most 8: rows R0..R0+7 fill half of the MFMA's 16
+// B-operand lanes and the tokens half of the A-operand lanes, so a plain
+// 16-row load reads 512 useful bytes per KiB of lanes. Here each weight and
+// act load carries two k-steps: lane l reads row (token) l%8 of k-step
+// 2j + (l/8)%2, columns (l/16)*8 .. +7, and a DPP row rotation by 8 moves the
+// second k-step into lanes l%16 < 8 for its MFMA. The other lanes' products
+// land in output rows / columns that are discarded. Same result as phase_down
+// (same k order per wave), with twice the bytes in flight per register.
+template <int MT>
+__device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
+  static_assert(MT == 1, "one token tile");
+  const BParams& p = *c.p;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  const bool last = li == p.n_layers - 1;
+  int R0, R1;
+  share(H, c.G, c.w, R0, R1);
+  constexpr int KW = INTER / NWAVE;       // 2048 columns per wave
+  constexpr int UPT = KW / (DKS * 32);    // 8 units (one tile)
+  constexpr int NP = DKS / 2;             // k-step pairs per unit
+  constexpr int NR = MK_BDN_RING;
+  static_assert(UPT % NR == 0 && MK_BDN_PRE <= NR, "down ring");
+  const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
+  const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)((c.B + 15) / 16 * 16) * INTER * 2);
+  // this lane's row / token, k-step of its pair and 8-column chunk
+  const int r8 = lane & 7, kh = (lane >> 3) & 1, ch = lane >> 4;
+  const int n = R0 + r8;
+  uint32_t wo;
+  if (p.tiled) {
+    constexpr uint32_t kb = INTER / 32;   // k-steps (1 KiB blocks) per 16-row tile
+    wo = (((uint32_t)n >> 4) * kb + (uint32_t)kh) * 1024u + (uint32_t)ch * 256u + (uint32_t)(n & 15) * 16u;
+  } else {
+    wo = (uint32_t)n * (INTER * 2) + (uint32_t)(kh * 32 + ch * 8) * 2u;
+  }
+  if (n >= R1) wo = OOB;
+  const uint32_t wstep = p.tiled ? 1024u : 64u;   // per k-step
+  const uint32_t ao = r8 < c.B ? (uint32_t)kh * 1024u + (uint32_t)(ch * 16 + r8) * 16u : OOB;
+  struct Unit {
+    u32x4 w[NP];
+    u32x4 a[NP];
+  };
+  auto issue_w = [&](int u, Unit& un) {
+    const int ks0 = (wave * KW + u * DKS * 32) >> 5;   // first k-step of the unit
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+      un.w[j] = ld_stream(rw, u < UPT ? wo + (uint32_t)(ks0 + 2 * j) * wstep : OOB);
+  };
+  auto issue_a = [&](int u, Unit& un) {
+    const int ks0 = (wave * KW + u * DKS * 32) >> 5;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) un.a[j] = ld16(ra, u < UPT ? ao + (uint32_t)(ks0 + 2 * j) * 1024u : OOB);
+  };
+  Unit ring[NR];
+#pragma unroll
+  for (int s = 0; s < MK_BDN_PRE; ++s) issue_w(s, ring[s]);
+  trace_mark(c.s, 2 * xk(li, 5) - 1);
+  wait_grid(c, li, HO_ACT);
+  trace_mark(c.s, 2 * xk(li, 5));
+#pragma unroll
+  for (int s = 0; s < NR; ++s) {
+    if (s >= MK_BDN_PRE) issue_w(s, ring[s]);
+    issue_a(s, ring[s]);
+  }
+  f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto unit = [&](int u, Unit& un) {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const u32x4 b0 = un.w[j], a0 = un.a[j];
+      const u32x4 b1 = {dpp_u32<DPP_ROR8>(b0.x), dpp_u32<DPP_ROR8>(b0.y), dpp_u32<DPP_ROR8>(b0.z),
+                        dpp_u32<DPP_ROR8>(b0.w)};
+      const u32x4 a1 = {dpp_u32<DPP_ROR8>(a0.x), dpp_u32<DPP_ROR8>(a0.y), dpp_u32<DPP_ROR8>(a0.z),
+                        dpp_u32<DPP_ROR8>(a0.w)};
+      acc[0] = mfma16(a0, b0, acc[0]);
+      acc[0] = mfma16(a1, b1, acc[0]);
+    }
+    issue_w(u + NR, un);
+    issue_a(u + NR, un);
+  };
+  for (int u = 0; u < UPT; u += NR) {
+#pragma unroll
+    for (int s = 0; s < NR; ++s) unit(u + s, ring[s]);
+  }
+  uint16_t* h2 = c.xb(li, p.lay.h2);
+  const f32x4 d = reduce_waves<MT>(acc, L);
+  if (wave == 0) {
+    const int row = R0 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = (lane >> 4) * 4 + i;
+      if (row < R1 && m < c.B) {
+        const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i]));
+        st_dev(h2 + (size_t)m * H + row, hv);
+        if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
+      }
+    }
+  }
+  lds_sync();
+  arrive(c.ho(li, HO_H2), c.w % N_SUB);
+  trace_done(c.s, li, 4);
+}
+
 // Down projection as a 2-D split: workgroup w computes the rows of row group
 // n = w / 4 over the K quarter kq = w % 4 (split over the 4 waves as above), so
 // it reads a quarter of act instead of all of it and fills whole 16-row tiles.
@@ -1277,6 +1388,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.dng = c.G / DN_KQ;
   c.drpg = c.dng > 0 ? H / c.dng : 0;
   // (batch 8 measured slower with it: there act is small and the extra hand-over costs more)
+  c.dpair = (H + c.G - 1) / c.G <= 8;
   c.d2 = MK_BDOWN_2D && (MT == 2 || MK_BDOWN_2D_MT1) && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
          c.drpg <= RES_MAX;
   c.sset = p.xch + p.lay.sent_base + (size_t)(epoch & 1u) * p.lay.sset;
@@ -1312,8 +1424,14 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
       phase_attn<MT>(c, li, L);
       phase_o<MT>(c, li, L);
       phase_gu<MT>(c, li, L);
-      if (c.d2) phase_down2d<MT>(c, li, L);
-      else phase_down<MT>(c, li, L);
+      if (c.d2) {
+        phase_down2d<MT>(c, li, L);
+      } else if constexpr (MT == 1 && MK_BDN_PAIR) {
+        if (c.dpair && c.B <= 8) phase_down_pair<MT>(c, li, L);
+        else phase_down<MT>(c, li, L);
+      } else {
+        phase_down<MT>(c, li, L);
+      }
       if (li + 1 < p.n_layers) {
         u32x4 wn[KS];
         phase_qkv<MT, false>(c, li + 1, L, wn);
