@@ -78,6 +78,9 @@
 #ifndef MK_BGU_CH
 #define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
 #endif
+#ifndef MK_BGU_CH_O
+#define MK_BGU_CH_O 4      // its copies per wave per poll round of the attention-output wait (O phase)
+#endif
 #ifndef MK_BDN_PAIR
 #define MK_BDN_PAIR 1      // 8-row down shares: each operand load carries two k-steps
 #endif
@@ -789,7 +792,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
 
 // O projection (split-K, A = attention output read in MFMA layout) + residual -> h1.
 template <int MT>
-__device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
+__device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& guc) {
   const BParams& p = *c.p;
   const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
   int R0, R1;
@@ -800,7 +803,11 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
   load_w<KS>(rw, p.tiled, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
   trace_mark(c.s, 2 * xk(li, 3) - 1);
   // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % N_SUB
-  wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
+  if constexpr (BLds<MT>::GW > 1 && MK_BGU_CH_O > 0)
+    wait_handover_copy(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB, guc, MK_BGU_CH_O,
+                       &L.gw[wave * KS * 64]);
+  else
+    wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
   trace_mark(c.s, 2 * xk(li, 3));
   u32x4 a[MT * KS];
   load_a_tiled<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)((c.B + 15) / 16 * 16) * H * 2), c.B, H / 32, wave * KQ, a);
@@ -826,9 +833,25 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L) {
   trace_done(c.s, li, 2);
 }
 
+// The LDS copy of the last weight unit of the wave's gate/up tile of run-layer
+// li (one token tile and exactly one tile per wave; otherwise no copy). It is
+// started in the O phase's wait for the attention output and finished in the
+// gate/up phase's h1 wait.
+template <int MT>
+__device__ __forceinline__ void gu_copy_init(const BCtx& c, int li, UnitCopy& uc) {
+  const BParams& p = *c.p;
+  int U0, U1;
+  share(INTER, c.G, c.w, U0, U1);
+  const int row0 = 2 * U0, row_end = 2 * U1, ntile = (row_end - row0 + 15) / 16, wave = wave_id();
+  const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
+  const rsrc_t rw = make_rsrc(p.w_gu + (size_t)(p.first_layer + li) * 2 * INTER * H, GU_LAYER_BYTES);
+  uc.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (H / (KS * 32) - 1) * KS * 32,
+          BLds<MT>::GW > 1 && my_tiles == 1);
+}
+
 // RMSNorm(h1) -> gate/up GEMM (whole tiles per wave) -> silu(gate) * up -> act.
 template <int MT>
-__device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
+__device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, UnitCopy& uc) {
   const BParams& p = *c.p;
   const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
   int U0, U1, R0, R1;
@@ -845,13 +868,12 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L) {
   };
   u32x4 wa[KS], wb[KS];
   // With one token tile, a wave with one weight tile takes that tile's last
-  // unit from an LDS copy made during the h1 wait (HBM is mostly idle then);
-  // the copies the wait leaves are issued behind the staging.
+  // unit from the LDS copy `uc` (gu_copy_init), made during the waits for the
+  // attention output and h1 (HBM is mostly idle then); the copies those waits
+  // leave are issued behind the staging.
   constexpr bool GL = BLds<MT>::GW > 1;
   static_assert(UPT == 4, "gate/up unit schedule");
   const bool gl = GL && nunits == UPT;
-  UnitCopy uc;
-  if (GL) uc.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (UPT - 1) * KS * 32, gl);
   u32x4* gdst = &L.gw[GL ? wave * KS * 64 : 0];
   // MK_BGU_PRE weight units are issued before the h1 wait, the others right
   // behind the h1 staging copies, so the staging does not queue behind them
@@ -1422,8 +1444,10 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     phase_qkv<MT, true>(c, 0, L, wv);
     for (int li = 0; li < p.n_layers; ++li) {
       phase_attn<MT>(c, li, L);
-      phase_o<MT>(c, li, L);
-      phase_gu<MT>(c, li, L);
+      UnitCopy guc;
+      gu_copy_init<MT>(c, li, guc);
+      phase_o<MT>(c, li, L, guc);
+      phase_gu<MT>(c, li, L, guc);
       if (c.d2) {
         phase_down2d<MT>(c, li, L);
       } else if constexpr (MT == 1 && MK_BDN_PAIR) {
