@@ -81,6 +81,9 @@
 #ifndef MK_BGU_CH_O
 #define MK_BGU_CH_O 4      // its copies per wave per poll round of the attention-output wait (O phase)
 #endif
+#ifndef MK_BO_PAIR
+#define MK_BO_PAIR 1       // 8-row O shares at batches up to 8: each operand load carries two k-steps
+#endif
 #ifndef MK_BDN_PAIR
 #define MK_BDN_PAIR 1      // 8-row down shares: each operand load carries two k-steps
 #endif
@@ -522,6 +525,42 @@ __device__ __forceinline__ void mma_reg(const u32x4 (&a)[MT * N], const u32x4 (&
     for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16(a[mt * N + s], wv[s], acc[mt]);
 }
 
+// Paired operand loads, for a workgroup with at most 8 weight rows R0.. and at
+// most 8 tokens (one token tile): rows (tokens) fill only half of the MFMA's 16
+// operand lanes, so a plain load reads 512 useful bytes per KiB of lanes. Here
+// lane l reads weight row R0 + l%8 (token l%8) of k-step 2j + (l/8)%2, columns
+// (l/16)*8 .. +7: one load carries the operands of two k-steps, and mfma_pair
+// moves the second into lanes l%16 < 8 with a DPP row rotation by 8. The other
+// lanes' products land in output rows / columns that are discarded.
+// Lane offset of k-step 0 in a weight matrix of row_bytes per row (rows >= R1
+// out of range); k-step ks adds ks * pair_wstep.
+__device__ __forceinline__ uint32_t pair_w_off(bool tiled, int R0, int R1, uint32_t row_bytes) {
+  const int lane = lane_id(), n = R0 + (lane & 7), kh = (lane >> 3) & 1, ch = lane >> 4;
+  uint32_t o;
+  if (tiled) {
+    const uint32_t kb = row_bytes / 64u;   // k-steps (1 KiB blocks) per 16-row tile
+    o = (((uint32_t)n >> 4) * kb + (uint32_t)kh) * 1024u + (uint32_t)ch * 256u + (uint32_t)(n & 15) * 16u;
+  } else {
+    o = (uint32_t)n * row_bytes + (uint32_t)(kh * 32 + ch * 8) * 2u;
+  }
+  return n < R1 ? o : OOB;
+}
+__device__ __forceinline__ uint32_t pair_wstep(bool tiled) { return tiled ? 1024u : 64u; }
+// Lane offset of k-step 0 in a matrix in A-tile order (a_tile_off; tokens >= B
+// out of range); k-step ks adds ks * 1024.
+__device__ __forceinline__ uint32_t pair_a_off(int B) {
+  const int lane = lane_id(), t = lane & 7, kh = (lane >> 3) & 1, ch = lane >> 4;
+  return t < B ? (uint32_t)kh * 1024u + (uint32_t)(ch * 16 + t) * 16u : OOB;
+}
+__device__ __forceinline__ f32x4 mfma_pair(u32x4 a0, u32x4 b0, f32x4 acc) {
+  const u32x4 a1 = {dpp_u32<DPP_ROR8>(a0.x), dpp_u32<DPP_ROR8>(a0.y), dpp_u32<DPP_ROR8>(a0.z),
+                    dpp_u32<DPP_ROR8>(a0.w)};
+  const u32x4 b1 = {dpp_u32<DPP_ROR8>(b0.x), dpp_u32<DPP_ROR8>(b0.y), dpp_u32<DPP_ROR8>(b0.z),
+                    dpp_u32<DPP_ROR8>(b0.w)};
+  acc = mfma16(a0, b0, acc);
+  return mfma16(a1, b1, acc);
+}
+
 // Sum of the 4 waves' partial tiles (fixed order); waves < MT receive the
 // full tile of token tile `wave`. The caller synchronises before L.red is reused.
 template <int MT>
@@ -799,8 +838,17 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
   share(H, c.G, c.w, R0, R1);
   const int ntile = (R1 - R0 + 15) / 16;
   const rsrc_t rw = make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES);
+  // at most 8 rows and 8 tokens: paired operand loads (pair_w_off), half the loads
+  const bool pr = MT == 1 && MK_BO_PAIR && c.dpair && c.B <= 8;
+  const uint32_t wo = pair_w_off(p.tiled, R0, R1, H * 2), wstep = pair_wstep(p.tiled);
+  const int ks0 = wave * (KQ / 32);
   u32x4 wv[KS];
-  load_w<KS>(rw, p.tiled, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
+  if (pr) {
+#pragma unroll
+    for (int j = 0; j < KS / 2; ++j) wv[j] = ld_stream(rw, wo + (uint32_t)(ks0 + 2 * j) * wstep);
+  } else {
+    load_w<KS>(rw, p.tiled, ntile > 0 ? R0 : R1, R1, H * 2, wave * KQ, wv);
+  }
   trace_mark(c.s, 2 * xk(li, 3) - 1);
   // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % N_SUB
   if constexpr (BLds<MT>::GW > 1 && MK_BGU_CH_O > 0)
@@ -809,9 +857,34 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
   else
     wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
   trace_mark(c.s, 2 * xk(li, 3));
-  u32x4 a[MT * KS];
-  load_a_tiled<MT, KS>(make_rsrc(c.xb(li, p.lay.att), (size_t)((c.B + 15) / 16 * 16) * H * 2), c.B, H / 32, wave * KQ, a);
+  const rsrc_t ratt = make_rsrc(c.xb(li, p.lay.att), (size_t)((c.B + 15) / 16 * 16) * H * 2);
   uint16_t* h1 = c.xb(li, p.lay.h1);
+  if (pr) {
+    const uint32_t ao = pair_a_off(c.B);
+    u32x4 a[KS / 2];
+#pragma unroll
+    for (int j = 0; j < KS / 2; ++j) a[j] = ld16(ratt, ao + (uint32_t)(ks0 + 2 * j) * 1024u);
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KS / 2; ++j) acc[0] = mfma_pair(a[j], wv[j], acc[0]);
+    const f32x4 d = reduce_waves<MT>(acc, L);
+    if (wave == 0) {
+      const int row = R0 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = (lane >> 4) * 4 + i;
+        if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i])));
+      }
+    }
+    lds_sync();
+    arrive(c.ho(li, HO_H1), c.w % N_SUB);
+    trace_done(c.s, li, 2);
+    return;
+  }
+  u32x4 a[MT * KS];
+  load_a_tiled<MT, KS>(ratt, c.B, H / 32, wave * KQ, a);
   for (int tt = 0; tt < ntile; ++tt) {
     f32x4 acc[MT];
 #pragma unroll
@@ -1000,14 +1073,9 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
 }
 
 // The down projection of a workgroup with at most 8 rows (a 256-workgroup
-// grid) at batches of at most 8: rows R0..R0+7 fill half of the MFMA's 16
-// B-operand lanes and the tokens half of the A-operand lanes, so a plain
-// 16-row load reads 512 useful bytes per KiB of lanes. Here each weight and
-// act load carries two k-steps: lane l reads row (token) l%8 of k-step
-// 2j + (l/8)%2, columns (l/16)*8 .. +7, and a DPP row rotation by 8 moves the
-// second k-step into lanes l%16 < 8 for its MFMA. The other lanes' products
-// land in output rows / columns that are discarded. Same result as phase_down
-// (same k order per wave), with twice the bytes in flight per register.
+// grid) at batches of at most 8, with paired operand loads (pair_w_off): same
+// result as phase_down (same k order per wave), with twice the bytes in
+// flight per register.
 template <int MT>
 __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   static_assert(MT == 1, "one token tile");
@@ -1023,19 +1091,8 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   static_assert(UPT % NR == 0 && MK_BDN_PRE <= NR, "down ring");
   const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
   const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)((c.B + 15) / 16 * 16) * INTER * 2);
-  // this lane's row / token, k-step of its pair and 8-column chunk
-  const int r8 = lane & 7, kh = (lane >> 3) & 1, ch = lane >> 4;
-  const int n = R0 + r8;
-  uint32_t wo;
-  if (p.tiled) {
-    constexpr uint32_t kb = INTER / 32;   // k-steps (1 KiB blocks) per 16-row tile
-    wo = (((uint32_t)n >> 4) * kb + (uint32_t)kh) * 1024u + (uint32_t)ch * 256u + (uint32_t)(n & 15) * 16u;
-  } else {
-    wo = (uint32_t)n * (INTER * 2) + (uint32_t)(kh * 32 + ch * 8) * 2u;
-  }
-  if (n >= R1) wo = OOB;
-  const uint32_t wstep = p.tiled ? 1024u : 64u;   // per k-step
-  const uint32_t ao = r8 < c.B ? (uint32_t)kh * 1024u + (uint32_t)(ch * 16 + r8) * 16u : OOB;
+  const uint32_t wo = pair_w_off(p.tiled, R0, R1, INTER * 2), wstep = pair_wstep(p.tiled);
+  const uint32_t ao = pair_a_off(c.B);
   struct Unit {
     u32x4 w[NP];
     u32x4 a[NP];
@@ -1065,15 +1122,7 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
   auto unit = [&](int u, Unit& un) {
 #pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      const u32x4 b0 = un.w[j], a0 = un.a[j];
-      const u32x4 b1 = {dpp_u32<DPP_ROR8>(b0.x), dpp_u32<DPP_ROR8>(b0.y), dpp_u32<DPP_ROR8>(b0.z),
-                        dpp_u32<DPP_ROR8>(b0.w)};
-      const u32x4 a1 = {dpp_u32<DPP_ROR8>(a0.x), dpp_u32<DPP_ROR8>(a0.y), dpp_u32<DPP_ROR8>(a0.z),
-                        dpp_u32<DPP_ROR8>(a0.w)};
-      acc[0] = mfma16(a0, b0, acc[0]);
-      acc[0] = mfma16(a1, b1, acc[0]);
-    }
+    for (int j = 0; j < NP; ++j) acc[0] = mfma_pair(un.a[j], un.w[j], acc[0]);
     issue_w(u + NR, un);
     issue_a(u + NR, un);
   };
