@@ -69,6 +69,9 @@
 #ifndef MK_BLM_ODD
 #define MK_BLM_ODD 100     // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
 #endif
+#ifndef MK_BQKV_WNORM
+#define MK_BQKV_WNORM 1    // QKV: each wave normalises the K quarter it multiplies, in registers
+#endif
 #ifndef MK_BATT_ROUNDS
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
 #endif
@@ -159,6 +162,7 @@ struct BLds {
   int ng[BATCH_MAX];         // attention plan: 128-row groups per kv head of each sequence
   int cum[BATCH_MAX + 1];    // attention plan: first item of each sequence
   int flag;
+  float ssq[NWAVE][16 * MT];   // QKV: each wave's sum of squares of every row over its K quarter
   // gate/up with one token tile: the last weight unit of each wave's tile,
   // copied from HBM while the workgroup waits for h1 (k-step s of wave w at
   // gw[(w*KS + s)*64], lane l's 16 bytes at + l, the register unit's lane
@@ -504,6 +508,61 @@ __device__ __forceinline__ void stage_finish(const BCtx& c, const uint16_t* gamm
   lds_sync();
 }
 
+// The QKV input staged (the copies before the AFTER last loads have landed),
+// raw: the raw columns [r0, r1) copied to L.res as stage_finish does; the
+// normalisation is qkv_norm_a's.
+template <int MT, int AFTER>
+__device__ __forceinline__ void stage_wait_raw(const BCtx& c, int r0, int r1, BLds<MT>& L) {
+  wait_vm_after<AFTER>();
+  lds_sync();
+  const int w = r1 - r0;
+  for (int i = threadIdx.x; i < c.B * w; i += NT) L.res[i / w][i % w] = L.xn[i / w][r0 + i % w];
+}
+// The A operands of the QKV split-K MFMA (wave w: the K quarter [512w, 512w+512)
+// of every row, in mma_lds's lane layout: a[mt*KS + s]) read from the raw
+// staged rows and RMS-normalised in registers: x_n = bf16(x * rsqrt(mean(x^2) +
+// eps)), the value norm_rows writes (gamma folded into the weights). Each
+// wave sums the squares of its quarter from the operands it already holds (the
+// 4 lanes of a row cover its 4 column chunks), the 4 waves' row sums meet in
+// L.ssq (one barrier, summed in wave order), and each element is scaled by
+// the lane that feeds it to the MFMA: no LDS write-back, no second barrier.
+template <int MT>
+__device__ __forceinline__ void qkv_norm_a(BLds<MT>& L, u32x4 (&a)[MT * KS]) {
+  const int wave = wave_id(), lane = lane_id(), k0 = wave * KQ;
+  float sa[MT], sb[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) sa[mt] = sb[mt] = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      a[mt * KS + s] = *reinterpret_cast<const u32x4*>(&L.xn[mt * 16 + (lane & 15)][k0 + s * 32 + (lane >> 4) * 8]);
+      if (s & 1) sb[mt] = dot8(a[mt * KS + s], a[mt * KS + s], sb[mt]);
+      else sa[mt] = dot8(a[mt * KS + s], a[mt * KS + s], sa[mt]);
+    }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float ss = add_xor32(add_xor16(sa[mt] + sb[mt]));   // row mt*16 + lane%16, this wave's quarter
+    if (lane < 16) L.ssq[wave][mt * 16 + lane] = ss;
+  }
+  lds_sync();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = mt * 16 + (lane & 15);
+    const float ss = ((L.ssq[0][r] + L.ssq[1][r]) + L.ssq[2][r]) + L.ssq[3][r];
+    const float inv = rsqrtf(ss * (1.0f / H) + EPS);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 x = a[mt * KS + s];
+      const uint32_t e[4] = {x.x, x.y, x.z, x.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = cvt_bf2(bf_lo(e[k]) * inv, bf_hi(e[k]) * inv);
+      a[mt * KS + s] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
 // One unit of MFMAs: KS k-steps from column k0, A from the staged LDS matrix.
 template <int MT>
 __device__ __forceinline__ void mma_lds(const BLds<MT>& L, int k0, const u32x4 (&wv)[KS], f32x4 (&acc)[MT]) {
@@ -674,20 +733,29 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L, u32x4 (&
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (!FIRST) {
     wait_h2(c, li - 1);
-    stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+    if (MK_BQKV_WNORM) {
+      stage_issue<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, L);
+      stage_wait_raw<MT, 0>(c, R0, R1, L);
+    } else {
+      stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
+    }
   } else {   // the first layer: its input is final data; the plan runs while it lands
     if (p.hidden_in) stage_issue<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, L);
     else stage_issue<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, L);
     if (MT == 1) plan_and_rope<MT>(c, L);   // (two tiles: in the prologue; inlined here it spills)
-    stage_finish<MT, 0>(c, nullptr, R0, R1, L);
+    if (MK_BQKV_WNORM) stage_wait_raw<MT, 0>(c, R0, R1, L);
+    else stage_finish<MT, 0>(c, nullptr, R0, R1, L);
   }
+  u32x4 an[MK_BQKV_WNORM ? MT * KS : 1];
+  if constexpr (MK_BQKV_WNORM) qkv_norm_a<MT>(L, an);
   trace_mark(c.s, 2 * xk(li, 1));
   uint16_t* xq = c.sx(li, p.lay.sq_qkv);
   for (int tt = 0; tt < ntile; ++tt) {
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mma_lds<MT>(L, wave * KQ, wv, acc);
+    if constexpr (MK_BQKV_WNORM) mma_reg<MT, KS>(an, wv, acc);
+    else mma_lds<MT>(L, wave * KQ, wv, acc);
     if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
     const f32x4 d = reduce_waves<MT>(acc, L);
     if (wave < MT) {
