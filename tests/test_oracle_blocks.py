@@ -1,4 +1,4 @@
-"""Pins the oracle's RMSNorm, attention and SwiGLU pieces.
+"""Pins the oracle's RMSNorm, attention and SwiGLU MLP pieces.
 
 Each check compares against something the mathematics fixes independently of
 the oracle's code: closed forms, brute force in float64 with Python loops on
@@ -138,8 +138,39 @@ def test_mk_attention_rounding_points():
     assert (got - exact).abs().max() < 1e-2
 
 
-def test_swiglu_closed_form():
-    x = torch.linspace(-6, 6, 101, dtype=torch.float64)
-    u = torch.linspace(2, -1, 101, dtype=torch.float64)
-    ref = x / (1 + torch.exp(-x)) * u
-    assert torch.allclose(torch.nn.functional.silu(x) * u, ref, rtol=1e-13, atol=1e-15)
+def test_oracle_mlp_is_swiglu_of_gate_and_up():
+    """The oracle's decoder layer, MLP half (mlp.py:98-192): with the attention's
+    output projection zero, layer(h) = h + W_d (silu(W_g n) * (W_u n)), n the
+    RMS-normalised h times the post-attention gamma. Checked in float64 against
+    Python loops with silu(x) = x / (1 + e^-x) written out, on random weights
+    where gate and up differ, so a swapped pair, silu on the wrong projection or
+    a transposed down projection fails."""
+    d = Dims(n_layers=1, hidden=8, n_q=2, n_kv=1, head_dim=4, inter=6, vocab=16)
+    g = torch.Generator().manual_seed(3)
+    r = lambda *shape: torch.randn(*shape, dtype=torch.float64, generator=g)
+    p = "layers.0."
+    sd = {
+        p + "input_layernorm.weight": 1.0 + 0.1 * r(8), p + "post_attention_layernorm.weight": 1.0 + 0.1 * r(8),
+        p + "self_attn.q_proj.weight": r(8, 8), p + "self_attn.k_proj.weight": r(4, 8),
+        p + "self_attn.v_proj.weight": r(4, 8), p + "self_attn.o_proj.weight": torch.zeros(8, 8, dtype=torch.float64),
+        p + "mlp.gate_proj.weight": r(6, 8), p + "mlp.up_proj.weight": r(6, 8), p + "mlp.down_proj.weight": r(8, 6),
+        "embed_tokens.weight": r(16, 8), "norm.weight": torch.ones(8, dtype=torch.float64),
+    }
+    o = OracleLlama(sd, d=d, mode="exact")
+    h = r(1, 8)
+    K, V = torch.zeros(1, 4, 4, dtype=torch.float64), torch.zeros(1, 4, 4, dtype=torch.float64)
+    got = o.layer(0, h, torch.tensor([0]), (K, V))[0]
+    x = [float(v) for v in h[0]]
+    ms = sum(v * v for v in x) / 8
+    gp = [float(v) for v in sd[p + "post_attention_layernorm.weight"]]
+    n = [x[i] / math.sqrt(ms + 1e-5) * gp[i] for i in range(8)]
+    Wg, Wu, Wd = (sd[p + f"mlp.{k}_proj.weight"].tolist() for k in ("gate", "up", "down"))
+    gate = [sum(Wg[j][i] * n[i] for i in range(8)) for j in range(6)]
+    up = [sum(Wu[j][i] * n[i] for i in range(8)) for j in range(6)]
+    act = [gate[j] / (1.0 + math.exp(-gate[j])) * up[j] for j in range(6)]
+    expect = torch.tensor([x[i] + sum(Wd[i][j] * act[j] for j in range(6)) for i in range(8)], dtype=torch.float64)
+    assert torch.allclose(got, expect, rtol=1e-12, atol=1e-12)
+    # the plausible miswirings give something else
+    swapped = [up[j] / (1.0 + math.exp(-up[j])) * gate[j] for j in range(6)]
+    bad = torch.tensor([x[i] + sum(Wd[i][j] * swapped[j] for j in range(6)) for i in range(8)], dtype=torch.float64)
+    assert (got - bad).abs().max() > 1e-3
