@@ -50,9 +50,9 @@ def new_caches(n_layers, s_max, device="cuda", fill=None, seed=0):
 
 
 def record_parity(name: str, data: dict) -> None:
-    """Write a test's measured parity numbers to gpurun_out/parity/<name>.json
-    (the directory comes back from a GPU run; profiles/parity_summary.md
-    cites these files)."""
+    """Write a test's measured parity numbers as <name>.json into the directory
+    MK_PARITY_DIR, else the repository's run-output folder (`parity/` under
+    it); the committed parity summary under profiles/ cites these files."""
     import json
     import os
     from pathlib import Path

@@ -24,7 +24,7 @@ cache (bf16 copied before the launch) with the same token and position, and:
   term into two), V within 1;
 * ``pos`` advanced by one per sequence.
 
-Measured numbers go to gpurun_out/parity/c4.json and c5.json.
+Measured numbers go to c4.json and c5.json (``record_parity`` in gpu_common).
 """
 
 import os
