@@ -76,7 +76,7 @@
 #define MK_BATT_ROUNDS 1   // attention ranges per workgroup
 #endif
 #ifndef MK_BGU_LDS
-#define MK_BGU_LDS 1       // one tile: the last gate/up weight unit copied to LDS during the h1 wait
+#define MK_BGU_LDS 1       // one tile: the last gate/up weight unit copied to LDS during the waits before it
 #endif
 #ifndef MK_BGU_CH
 #define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
@@ -164,7 +164,8 @@ struct BLds {
   int flag;
   float ssq[NWAVE][16 * MT];   // QKV: each wave's sum of squares of every row over its K quarter
   // gate/up with one token tile: the last weight unit of each wave's tile,
-  // copied from HBM while the workgroup waits for h1 (k-step s of wave w at
+  // copied from HBM while the workgroup waits for the attention output and
+  // for h1 (k-step s of wave w at
   // gw[(w*KS + s)*64], lane l's 16 bytes at + l, the register unit's lane
   // order), and a 1 KiB area per wave that copies past it write (two tiles
   // leave no room in LDS for either)
