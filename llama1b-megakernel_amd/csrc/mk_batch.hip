@@ -82,7 +82,10 @@
 #define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
 #endif
 #ifndef MK_BGU_CH_O
-#define MK_BGU_CH_O 4      // its copies per wave per poll round of the attention-output wait (O phase)
+#define MK_BGU_CH_O 8      // its copies per wave per poll round of the attention-output wait (O phase)
+#endif
+#ifndef MK_BGU_SKIP_O
+#define MK_BGU_SKIP_O 1    // failed polls of that wait before its copies start
 #endif
 #ifndef MK_BO_PAIR
 #define MK_BO_PAIR 1       // 8-row O shares at batches up to 8: each operand load carries two k-steps
@@ -328,7 +331,7 @@ struct UnitCopy {
 // wait_handover that issues `ch` more copies of `uc` after every poll that
 // finds the hand-over incomplete (the next poll queues behind them).
 __device__ __forceinline__ void wait_handover_copy(const Sync& sy, const uint32_t* ho, int per, int extra,
-                                                   UnitCopy& uc, int ch, u32x4* dst) {
+                                                   UnitCopy& uc, int ch, u32x4* dst, int skip = 0) {
   const int lane = lane_id();
   const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
   const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
@@ -338,7 +341,7 @@ __device__ __forceinline__ void wait_handover_copy(const Sync& sy, const uint32_
     const uint32_t v = ld_dev4(r, off);
     if (__all(v >= target)) return;
     if (wait_expired(sy, t0, it)) return;
-    uc.issue(ch, dst);
+    if (it > skip) uc.issue(ch, dst);
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -922,7 +925,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
   // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % N_SUB
   if constexpr (BLds<MT>::GW > 1 && MK_BGU_CH_O > 0)
     wait_handover_copy(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB, guc, MK_BGU_CH_O,
-                       &L.gw[wave * KS * 64]);
+                       &L.gw[wave * KS * 64], MK_BGU_SKIP_O);
   else
     wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
   trace_mark(c.s, 2 * xk(li, 3));
