@@ -641,6 +641,19 @@ __device__ __forceinline__ f32x4 reduce_waves(const f32x4 (&acc)[MT], BLds<MT>& 
   return d;
 }
 
+// The same sum (same order) of token tile mt, for any wave.
+template <int MT>
+__device__ __forceinline__ f32x4 reduce_tile(const f32x4 (&acc)[MT], BLds<MT>& L, int mt) {
+  const int wave = wave_id(), lane = lane_id();
+#pragma unroll
+  for (int m = 0; m < MT; ++m) L.red[wave][m][lane] = acc[m];
+  lds_sync();
+  f32x4 d = L.red[0][mt][lane];
+#pragma unroll
+  for (int w = 1; w < NWAVE; ++w) d += L.red[w][mt][lane];
+  return d;
+}
+
 // ---------------------------------------------------------------------------
 // Phases
 // ---------------------------------------------------------------------------
@@ -761,16 +774,23 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L, u32x4 (&
     if constexpr (MK_BQKV_WNORM) mma_reg<MT, KS>(an, wv, acc);
     else mma_lds<MT>(L, wave * KQ, wv, acc);
     if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
-    const f32x4 d = reduce_waves<MT>(acc, L);
-    if (wave < MT) {
+    // every wave finishes a share of the outputs: token tile wave % MT, and
+    // IPW of the 4 output rows of each lane (rows (lane/16)*4 + i of the tile)
+    constexpr int IPW = 4 * MT / NWAVE;
+    static_assert(IPW >= 1 && 4 * MT % NWAVE == 0, "QKV epilogue split");
+    const int mtw = wave % MT, i0 = (wave / MT) * IPW;
+    const f32x4 d = reduce_tile<MT>(acc, L, mtw);
+    {
       const int row = row0 + tt * 16 + (lane & 15);
       const bool rv = row < row_end;
       const int pr = row >> 1, dd = pr & 31, hi = row & 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float mine = rbf(d[i]);
+      for (int ii = 0; ii < IPW; ++ii) {
+        const int i = i0 + ii;
+        const float di = i == 0 ? d[0] : i == 1 ? d[1] : i == 2 ? d[2] : d[3];
+        const float mine = rbf(di);
         const float other = dpp<DPP_XOR1>(mine);   // the pair partner (row ^ 1)
-        const int m = wave * 16 + (lane >> 4) * 4 + i;
+        const int m = mtw * 16 + (lane >> 4) * 4 + i;
         if (!rv || m >= c.B) continue;
         const float a = hi ? other : mine, b = hi ? mine : other;   // elements d, d+32
         const int ps = L.pos[m];
