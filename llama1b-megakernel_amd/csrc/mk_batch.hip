@@ -624,24 +624,8 @@ __device__ __forceinline__ f32x4 mfma_pair(u32x4 a0, u32x4 b0, f32x4 acc) {
   return mfma16(a1, b1, acc);
 }
 
-// Sum of the 4 waves' partial tiles (fixed order); waves < MT receive the
-// full tile of token tile `wave`. The caller synchronises before L.red is reused.
-template <int MT>
-__device__ __forceinline__ f32x4 reduce_waves(const f32x4 (&acc)[MT], BLds<MT>& L) {
-  const int wave = wave_id(), lane = lane_id();
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) L.red[wave][mt][lane] = acc[mt];
-  lds_sync();
-  f32x4 d = {0.f, 0.f, 0.f, 0.f};
-  if (wave < MT) {
-    d = L.red[0][wave][lane];
-#pragma unroll
-    for (int w = 1; w < NWAVE; ++w) d += L.red[w][wave][lane];
-  }
-  return d;
-}
-
-// The same sum (same order) of token tile mt, for any wave.
+// Sum of the 4 waves' partial tiles of token tile mt (fixed order, wave 0
+// first), for any wave. The caller synchronises before L.red is reused.
 template <int MT>
 __device__ __forceinline__ f32x4 reduce_tile(const f32x4 (&acc)[MT], BLds<MT>& L, int mt) {
   const int wave = wave_id(), lane = lane_id();
@@ -652,6 +636,38 @@ __device__ __forceinline__ f32x4 reduce_tile(const f32x4 (&acc)[MT], BLds<MT>& L
 #pragma unroll
   for (int w = 1; w < NWAVE; ++w) d += L.red[w][mt][lane];
   return d;
+}
+
+// A reduced tile's outputs: f(m, v) gets the token m (in the batch) and the
+// summed value (reduce_tile's) of each of a lane's 4 output rows (lane/16)*4 + i.
+// SPREAD: every wave finishes a share (wave w: token tile w % MT, 4*MT/4 of the
+// rows); otherwise wave w < MT finishes all of token tile w (measured better
+// with two tiles, where the share is two rows).
+template <int MT, bool SPREAD, class F>
+__device__ __forceinline__ void tile_out(const f32x4 (&acc)[MT], BLds<MT>& L, F&& f) {
+  const int wave = wave_id(), lane = lane_id();
+  if (SPREAD) {
+    constexpr int IPW = 4 * MT / NWAVE;
+    static_assert(IPW >= 1 && 4 * MT % NWAVE == 0, "tile output split");
+    const int mtw = wave % MT, i0 = (wave / MT) * IPW;
+    const f32x4 d = reduce_tile<MT>(acc, L, mtw);
+#pragma unroll
+    for (int ii = 0; ii < IPW; ++ii) {
+      const int i = i0 + ii;
+      f(mtw * 16 + (lane >> 4) * 4 + i, i == 0 ? d[0] : i == 1 ? d[1] : i == 2 ? d[2] : d[3]);
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) L.red[wave][mt][lane] = acc[mt];
+    lds_sync();
+    if (wave < MT) {
+      f32x4 d = L.red[0][wave][lane];
+#pragma unroll
+      for (int w = 1; w < NWAVE; ++w) d += L.red[w][wave][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f(wave * 16 + (lane >> 4) * 4 + i, d[i]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -961,15 +977,10 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KS / 2; ++j) acc[0] = mfma_pair(a[j], wv[j], acc[0]);
-    const f32x4 d = reduce_waves<MT>(acc, L);
-    if (wave == 0) {
-      const int row = R0 + (lane & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = (lane >> 4) * 4 + i;
-        if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i])));
-      }
-    }
+    const int row = R0 + (lane & 15);
+    tile_out<MT, true>(acc, L, [&](int m, float v) {
+      if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(v)));
+    });
     lds_sync();
     arrive(c.ho(li, HO_H1), c.w % N_SUB);
     trace_done(c.s, li, 2);
@@ -983,15 +994,10 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mma_reg<MT, KS>(a, wv, acc);
     if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, R0 + 16 * (tt + 1), R1, H * 2, wave * KQ, wv);
-    const f32x4 d = reduce_waves<MT>(acc, L);
-    if (wave < MT) {
-      const int row = R0 + tt * 16 + (lane & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = wave * 16 + (lane >> 4) * 4 + i;
-        if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i])));
-      }
-    }
+    const int row = R0 + tt * 16 + (lane & 15);
+    tile_out<MT, false>(acc, L, [&](int m, float v) {
+      if (row < R1 && m < c.B) st_dev(h1 + (size_t)m * H + row, f2bf(bf2f(L.res[m][row - R0]) + rbf(v)));
+    });
     lds_sync();
   }
   arrive(c.ho(li, HO_H1), c.w % N_SUB);
@@ -1140,19 +1146,14 @@ __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
     issue_w(u + 2, un);
     issue_a(u + 2, un);
     if (u % UPT == UPT - 1) {
-      const f32x4 d = reduce_waves<MT>(acc, L);
-      if (wave < MT) {
-        const int row = R0 + (u / UPT) * 16 + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = wave * 16 + (lane >> 4) * 4 + i;
-          if (row < R1 && m < c.B) {
-            const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i]));
-            st_dev(h2 + (size_t)m * H + row, hv);
-            if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
-          }
+      const int row = R0 + (u / UPT) * 16 + (lane & 15);
+      tile_out<MT, false>(acc, L, [&](int m, float v) {
+        if (row < R1 && m < c.B) {
+          const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(v));
+          st_dev(h2 + (size_t)m * H + row, hv);
+          if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
         }
-      }
+      });
       lds_sync();
     }
   };
@@ -1223,19 +1224,14 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
     for (int s = 0; s < NR; ++s) unit(u + s, ring[s]);
   }
   uint16_t* h2 = c.xb(li, p.lay.h2);
-  const f32x4 d = reduce_waves<MT>(acc, L);
-  if (wave == 0) {
-    const int row = R0 + (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = (lane >> 4) * 4 + i;
-      if (row < R1 && m < c.B) {
-        const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(d[i]));
-        st_dev(h2 + (size_t)m * H + row, hv);
-        if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
-      }
+  const int row = R0 + (lane & 15);
+  tile_out<MT, true>(acc, L, [&](int m, float v) {
+    if (row < R1 && m < c.B) {
+      const uint32_t hv = f2bf(bf2f(L.res[m][row - R0]) + rbf(v));
+      st_dev(h2 + (size_t)m * H + row, hv);
+      if (last && p.hidden_out) p.hidden_out[(size_t)m * H + row] = (uint16_t)hv;
     }
-  }
+  });
   lds_sync();
   arrive(c.ho(li, HO_H2), c.w % N_SUB);
   trace_done(c.s, li, 4);
@@ -1289,15 +1285,10 @@ __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
     issue_w(u + 2, un);
     issue_a(u + 2, un);
     if (u % UPT == UPT - 1) {
-      const f32x4 d = reduce_waves<MT>(acc, L);
-      if (wave < MT) {
-        const int row = R0 + (u / UPT) * 16 + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = wave * 16 + (lane >> 4) * 4 + i;
-          if (m < c.B) st_dev(dp + ((size_t)kq * p.max_batch + m) * H + row, d[i]);
-        }
-      }
+      const int row = R0 + (u / UPT) * 16 + (lane & 15);
+      tile_out<MT, false>(acc, L, [&](int m, float v) {
+        if (m < c.B) st_dev(dp + ((size_t)kq * p.max_batch + m) * H + row, v);
+      });
       lds_sync();
     }
   };
