@@ -87,6 +87,9 @@
 #ifndef MK_BGU_SKIP_O
 #define MK_BGU_SKIP_O 1    // failed polls of that wait before its copies start
 #endif
+#ifndef MK_BGU_HALF
+#define MK_BGU_HALF 1      // at most 8 tokens: half of gate/up unit 2 copied to the staged matrix's padding rows
+#endif
 #ifndef MK_BO_PAIR
 #define MK_BO_PAIR 1       // 8-row O shares at batches up to 8: each operand load carries two k-steps
 #endif
@@ -283,10 +286,12 @@ __device__ __forceinline__ void wait_handover(const Sync& sy, const uint32_t* ho
 // few 1 KiB copies at a time, so that the copies fill the hand-over wait
 // before the unit is used without one burst of them queueing ahead of the
 // poll.
-struct UnitCopy {
+// (UnitCopyT<N>: the first N k-steps of such a unit, N x 1 KiB.)
+template <int N>
+struct UnitCopyT {
   rsrc_t r;
   uint32_t o, step;
-  int next;   // k-steps issued (KS: all, or no copy)
+  int next;   // k-steps issued (N: all, or no copy)
   __device__ __forceinline__ void init(rsrc_t rw, bool tiled, int row, int row_end, uint32_t row_bytes, int k0,
                                        bool on) {
     const int lane = lane_id();
@@ -301,11 +306,11 @@ struct UnitCopy {
     }
     if (n >= row_end) o = OOB;
     r = rw;
-    next = on ? 0 : KS;
+    next = on ? 0 : N;
   }
   // up to n more k-steps
   __device__ __forceinline__ void issue(int n, u32x4* dst) {
-    const int end = min(KS, next + n);
+    const int end = min(N, next + n);
     for (; next < end; ++next)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(dst + next * 64), 16, o + (uint32_t)next * step, 0, 0,
                                                AUX_NT);
@@ -320,18 +325,39 @@ struct UnitCopy {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int ck = nx + k;
-      const bool real = ck < KS;
+      const bool real = ck < N;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(real ? dst + ck * 64 : spare), 16,
                                                real ? o + (uint32_t)ck * step : OOB, 0, 0, AUX_NT);
     }
-    next = min(KS, nx + K);
+    next = min(N, nx + K);
+  }
+};
+using UnitCopy = UnitCopyT<KS>;
+
+// The gate/up weights a wave copies to LDS ahead of the gate/up phase (one
+// token tile, one weight tile per wave): u3, the tile's last unit, into gw;
+// u2, the first half of its unit 2, into rows 8..15 of the staged matrix when
+// the batch has at most 8 tokens (those rows are MFMA padding whose products
+// are discarded; the h1 staging then leaves them alone). issue(n) takes u3's
+// copies first.
+struct GuCopy {
+  UnitCopy u3;
+  UnitCopyT<KS / 2> u2;
+  u32x4* d3;
+  u32x4* d2;
+  bool half;   // u2 is live (workgroup-uniform)
+  __device__ __forceinline__ void issue(int n, u32x4*) {
+    const int before = u3.next;
+    u3.issue(n, d3);
+    u2.issue(n - (u3.next - before), d2);
   }
 };
 
 // wait_handover that issues `ch` more copies of `uc` after every poll that
 // finds the hand-over incomplete (the next poll queues behind them).
+template <class Copy>
 __device__ __forceinline__ void wait_handover_copy(const Sync& sy, const uint32_t* ho, int per, int extra,
-                                                   UnitCopy& uc, int ch, u32x4* dst, int skip = 0) {
+                                                   Copy& uc, int ch, u32x4* dst, int skip = 0) {
   const int lane = lane_id();
   const rsrc_t r = make_rsrc(ho, N_SUB * CNT_LINE);
   const uint32_t off = lane < N_SUB ? (uint32_t)(lane * CNT_LINE) : OOB;
@@ -417,15 +443,18 @@ __device__ __forceinline__ void load_a_tiled(rsrc_t r, int B, int kb, int k0, u3
 // (a fixed count, AFTER of them) are not waited for, since vector loads
 // complete in order.
 template <int MT>
-__device__ __forceinline__ void stage_issue(const BCtx& c, rsrc_t src, bool gather, BLds<MT>& L) {
+__device__ __forceinline__ void stage_issue(const BCtx& c, rsrc_t src, bool gather, BLds<MT>& L,
+                                            u32x4* hi_spare = nullptr) {
   const int wave = wave_id(), lane = lane_id();
-  // 1 KiB quarters of rows: wave w copies quarters w, w+4, ... (16*MT each)
+  // 1 KiB quarters of rows: wave w copies quarters w, w+4, ... (16*MT each);
+  // rows >= B read zero, into hi_spare instead when it is given
 #pragma unroll
   for (int j = 0; j < 16 * MT; ++j) {
     const int qi = j * NWAVE + wave, m = qi >> 2, qq = qi & 3;
     const uint32_t row = gather ? (uint32_t)L.tok[m < BATCH_MAX ? m : 0] : (uint32_t)m;
     const uint32_t off = m < c.B ? row * (uint32_t)(H * 2) + (uint32_t)(qq * 1024 + lane * 16) : OOB;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr_t)&L.xn[m][qq * 512], 16, off, 0, 0, 0);
+    void* dst = hi_spare && m >= c.B ? (void*)hi_spare : (void*)&L.xn[m][qq * 512];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_ptr_t)dst, 16, off, 0, 0, 0);
   }
   // no memory access may move above the copies: stage_finish counts on them
   // being the oldest loads in flight
@@ -939,7 +968,7 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
 
 // O projection (split-K, A = attention output read in MFMA layout) + residual -> h1.
 template <int MT>
-__device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& guc) {
+__device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, GuCopy& guc) {
   const BParams& p = *c.p;
   const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
   int R0, R1;
@@ -1009,20 +1038,24 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, UnitCopy& 
 // started in the O phase's wait for the attention output and finished in the
 // gate/up phase's h1 wait.
 template <int MT>
-__device__ __forceinline__ void gu_copy_init(const BCtx& c, int li, UnitCopy& uc) {
+__device__ __forceinline__ void gu_copy_init(const BCtx& c, int li, BLds<MT>& L, GuCopy& gc) {
   const BParams& p = *c.p;
   int U0, U1;
   share(INTER, c.G, c.w, U0, U1);
   const int row0 = 2 * U0, row_end = 2 * U1, ntile = (row_end - row0 + 15) / 16, wave = wave_id();
   const int my_tiles = ntile > wave ? (ntile - wave + NWAVE - 1) / NWAVE : 0;
   const rsrc_t rw = make_rsrc(p.w_gu + (size_t)(p.first_layer + li) * 2 * INTER * H, GU_LAYER_BYTES);
-  uc.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (H / (KS * 32) - 1) * KS * 32,
-          BLds<MT>::GW > 1 && my_tiles == 1);
+  constexpr bool GL = BLds<MT>::GW > 1;
+  gc.u3.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (H / (KS * 32) - 1) * KS * 32, GL && my_tiles == 1);
+  gc.half = GL && MK_BGU_HALF && c.B <= 8 && ntile == NWAVE;
+  gc.u2.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, 2 * KS * 32, gc.half);
+  gc.d3 = &L.gw[GL ? wave * KS * 64 : 0];
+  gc.d2 = reinterpret_cast<u32x4*>(&L.xn[MT == 1 ? 8 : 0][0]) + wave * (KS / 2) * 64;
 }
 
 // RMSNorm(h1) -> gate/up GEMM (whole tiles per wave) -> silu(gate) * up -> act.
 template <int MT>
-__device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, UnitCopy& uc) {
+__device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, GuCopy& gc) {
   const BParams& p = *c.p;
   const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
   int U0, U1, R0, R1;
@@ -1039,27 +1072,33 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, UnitCopy&
   };
   u32x4 wa[KS], wb[KS];
   // With one token tile, a wave with one weight tile takes that tile's last
-  // unit from the LDS copy `uc` (gu_copy_init), made during the waits for the
+  // unit from the LDS copy gc.u3 (gu_copy_init), made during the waits for the
   // attention output and h1 (HBM is mostly idle then); the copies those waits
   // leave are issued behind the staging.
   constexpr bool GL = BLds<MT>::GW > 1;
   static_assert(UPT == 4, "gate/up unit schedule");
   const bool gl = GL && nunits == UPT;
-  u32x4* gdst = &L.gw[GL ? wave * KS * 64 : 0];
+  u32x4* gdst = gc.d3;
+  u32x4* spare = &L.gspare[GL ? wave * 64 : 0];
+  // with at most 8 tokens, the first half of unit 2 is in LDS too (gc.u2)
+  const bool half = gl && gc.half;
   // MK_BGU_PRE weight units are issued before the h1 wait, the others right
   // behind the h1 staging copies, so the staging does not queue behind them
   if (MK_BGU_PRE >= 1) issue(0, wa);
   if (MK_BGU_PRE >= 2) issue(1, wb);
   trace_mark(c.s, 2 * xk(li, 4) - 1);
-  if (GL) wait_handover_copy(c.s, c.ho(li, HO_H1), c.G / N_SUB, c.G % N_SUB, uc, MK_BGU_CH, gdst);
+  if (GL) wait_handover_copy(c.s, c.ho(li, HO_H1), c.G / N_SUB, c.G % N_SUB, gc, MK_BGU_CH, gdst);
   else wait_grid(c, li, HO_H1);
-  stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L);
+  stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L, gc.half ? spare : nullptr);
   if (MK_BGU_PRE < 1) issue(0, wa);
   if (MK_BGU_PRE < 2) issue(1, wb);
-  if (GL) uc.issue_fixed<KS>(gdst, &L.gspare[GL ? wave * 64 : 0]);
+  if (GL) {
+    gc.u3.issue_fixed<KS>(gdst, spare);
+    gc.u2.issue_fixed<KS / 2>(gc.d2, spare);
+  }
   // the raw columns kept for the down projection's residual: its rows
   const int D0 = c.d2 ? (c.w / DN_KQ) * c.drpg : R0, D1 = c.d2 ? D0 + c.drpg : R1;
-  stage_finish<MT, (2 - MK_BGU_PRE) * KS + (GL ? KS : 0)>(c, nullptr, D0, D1, L);
+  stage_finish<MT, (2 - MK_BGU_PRE) * KS + (GL ? KS + KS / 2 : 0)>(c, nullptr, D0, D1, L);
   trace_mark(c.s, 2 * xk(li, 4));
   uint16_t* act = c.xb(li, p.lay.act);
   f32x4 acc[MT];
@@ -1085,7 +1124,19 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, UnitCopy&
         }
     }
   };
-  if (gl) {   // units 0-2 from registers (unit 2 issued after unit 0), unit 3 from LDS
+  if (half) {   // units 0, 1 and the second half of 2 from registers, the rest from LDS
+    unit(0, wa, false);
+    load_w<KS / 2>(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, 2 * KS * 32 + (KS / 2) * 32,
+                   *reinterpret_cast<u32x4(*)[KS / 2]>(&wa[KS / 2]));
+    unit(1, wb, false);
+    wait_mem();   // the copies were issued before these loads
+#pragma unroll
+    for (int s = 0; s < KS / 2; ++s) wa[s] = gc.d2[s * 64 + lane];
+    unit(2, wa, false);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) wa[s] = gdst[s * 64 + lane];
+    unit(3, wa, false);
+  } else if (gl) {   // units 0-2 from registers (unit 2 issued after unit 0), unit 3 from LDS
     unit(0, wa, true);
     unit(1, wb, false);
     unit(2, wa, false);
@@ -1576,8 +1627,8 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
     phase_qkv<MT, true>(c, 0, L, wv);
     for (int li = 0; li < p.n_layers; ++li) {
       phase_attn<MT>(c, li, L);
-      UnitCopy guc;
-      gu_copy_init<MT>(c, li, guc);
+      GuCopy guc;
+      gu_copy_init<MT>(c, li, L, guc);
       phase_o<MT>(c, li, L, guc);
       phase_gu<MT>(c, li, L, guc);
       if (c.d2) {
