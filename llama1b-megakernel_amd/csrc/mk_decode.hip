@@ -115,6 +115,10 @@ static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
 #endif
 constexpr int D_EARLY = MK_D_EARLY;
 static_assert(D_EARLY >= 0 && D_EARLY <= 16, "down-projection early chunks");
+// lm_head rows per wave in the register ring (4 KiB each)
+#ifndef MK_LM_RING
+#define MK_LM_RING 8
+#endif
 // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
 #ifndef MK_LM_ODD
 #define MK_LM_ODD 100
@@ -766,7 +770,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     if (p.do_lm) {
       int V0, V1;
       share_parity(VOCAB, G, w, 100, MK_LM_ODD, V0, V1);
-      RowStream<8, 4> ls;
+      RowStream<MK_LM_RING, 4> ls;
       const Span sp = wave_span(V0, V1);
       ls.start(make_rsrc(p.embed, EMBED_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
       trace_mark(c.s, 2 * xk(p.n_layers, 1) - 1);
