@@ -69,6 +69,9 @@
 #ifndef MK_BLM_ODD
 #define MK_BLM_ODD 100     // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
 #endif
+#ifndef MK_BLM_COLLECT
+#define MK_BLM_COLLECT 1   // one token tile: a workgroup's logits collected in LDS, stored after its last round
+#endif
 #ifndef MK_BQKV_WNORM
 #define MK_BQKV_WNORM 1    // QKV: each wave normalises the K quarter it multiplies, in registers
 #endif
@@ -1472,6 +1475,15 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   float (*stage)[64] = reinterpret_cast<float (*)[64]>(&L.red[0][0][0]);
   const rsrc_t rlog = make_rsrc(p.logits ? (const void*)p.logits : (const void*)p.lm,
                                 p.logits ? (size_t)c.B * VOCAB * 4 : 0);
+  // With one token tile the gate/up copy area (idle here) holds the logits of
+  // the whole share instead: each wave writes its tiles there, with no
+  // workgroup barrier per round, and the share leaves after the last round as
+  // one contiguous run per token
+  constexpr bool LGC = BLds<MT>::GW > 1 && MK_BLM_COLLECT;
+  constexpr int LG_ROWS = 512, LG_STRIDE = LG_ROWS + 4;   // +4 floats: the lane groups' tokens on distinct banks
+  static_assert(!LGC || sizeof(L.gw) >= sizeof(float) * 16 * MT * LG_STRIDE, "logit collection area");
+  const bool lgc = LGC && V1 - V0 <= LG_ROWS;
+  float* lgb = reinterpret_cast<float*>(&L.gw[0]);
   auto issue = [&](int u, u32x4(&wv)[KS]) {
     load_w<KS>(rw, p.tiled, u < nunits ? V0 + 16 * (wave + NWAVE * (u / UPT)) : V1, V1, H * 2, (u % UPT) * KS * 32, wv);
   };
@@ -1508,12 +1520,14 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
         for (int i = 0; i < 4; ++i) {
           const int m = mt * 16 + (lane >> 4) * 4 + i;
           const float v = acc[mt][i];
-          stage[m][wave * 16 + (lane & 15)] = v;
+          if (lgc) lgb[m * LG_STRIDE + (row - V0)] = v;   // row - V0 < 16 * 4 * ceil(ntile / 4) <= 512
+          else stage[m][wave * 16 + (lane & 15)] = v;
           if (row < V1 && m < c.B && v > best[mt][i]) {   // a lane's rows ascend: keeps the lowest index among equal maxima
             best[mt][i] = v;
             bidx[mt][i] = row;
           }
         }
+      if (lgc) return;
       lds_sync();
       {   // thread t: token t / 8, rows 8*(t % 8) .. +7 of the round
         const int t = threadIdx.x, m = t >> 3, r8 = (t & 7) * 8;
@@ -1554,6 +1568,16 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
     if (k != 0ull)
       __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(p.ws + BWS_KEY0 + (size_t)t * BWS_KEY_STRIDE), k,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (lgc) {   // (the barrier above made every wave's tiles visible) token m's rows [V0, V1) in 16-byte pieces
+    const int nq = (V1 - V0) / 4, q = t & 127;   // V0, V1 multiples of 8: nq <= 128
+    for (int m = t >> 7; m < c.B; m += 2) {
+      const float4 v = *reinterpret_cast<const float4*>(lgb + m * LG_STRIDE + 4 * q);
+      const uint32_t off = q < nq ? ((uint32_t)m * (uint32_t)VOCAB + (uint32_t)(V0 + 4 * q)) * 4u : OOB;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)}, rlog,
+          (int)off, 0, 0);
+    }
   }
 }
 
