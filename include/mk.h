@@ -247,11 +247,21 @@ int mk_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
  * a batched area, or keeps a batch-1 (uncached) area as a spare that the next
  * mk_workspace_init reuses (uncached memory a kernel has read is never freed
  * while the process runs). The workspace must be initialised again before its
- * next step. Lifecycle counterpart of mk_workspace_init; no counterpart in
+ * next step. A HIP graph that captured steps on the workspace holds the
+ * area's address in its kernel arguments and a replay does not check it, so
+ * release a workspace only after every such graph is destroyed, and never
+ * during a stream capture (the device synchronisation fails there:
+ * MK_ERR_HIP). Lifecycle counterpart of mk_workspace_init; no counterpart in
  * the reference.
  */
 int mk_workspace_release(void *workspace);
-/* Synchronise `stream`, return the device error bits and clear them. */
+/*
+ * Synchronise `stream`, return the device error bits of `workspace` and clear
+ * them. workspace == NULL: the sticky error bits of the current device's
+ * allocation-free scratch (every faulted mk_decode_step_noalloc step since the
+ * last such read; 0 before its first use), read and cleared with two small
+ * copies (no allocation by this library).
+ */
 int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);
 
 /* The decode step (see mk_step_args). Asynchronous on the stream. */
@@ -272,9 +282,11 @@ int mk_decode_step(const mk_weights *w, const mk_step_args *a);
  *     - batch must be 1 (MK_ERR_SHAPE otherwise) and MK_FLAG_PREFILL is
  *       refused (MK_ERR_UNSUPPORTED): the scratch holds batch-1 buffers only;
  *     - workspace must be NULL and workspace_bytes 0 (MK_ERR_WORKSPACE);
- *     - device-detected faults (MK_DEVERR_*) are not kept for
- *       mk_read_device_error: a faulted step writes next_token[0] = -1 (if
- *       next_token is given) and does not advance pos.
+ *     - device-detected faults (MK_DEVERR_*): a faulted step writes
+ *       next_token[0] = -1 (if next_token is given), does not advance pos,
+ *       and ORs its bits into a sticky word of the scratch that
+ *       mk_read_device_error(NULL, stream, &bits) returns and clears, so a
+ *       step without next_token (the layer-stack seam) reports its faults too.
  *   Every call of this entry point on one device shares that device's
  *   scratch, and each call leaves it ready for the next: calls that overlap
  *   in time on one device (e.g. on two unordered streams) race and give

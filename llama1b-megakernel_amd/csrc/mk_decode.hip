@@ -132,6 +132,7 @@ constexpr int MAX_GRID = 1024;
 // live in a separate uncached area (SET_BYTES each) tied to the workspace.
 constexpr size_t CTRL_BYTES = 256;
 constexpr int C_EXIT = 0, C_ERR = 1, C_EPOCH = 2;   // u32 words of the control block
+constexpr int C_STICKY = 3;   // allocation-free scratch only: error bits of every faulted step since the last read
 constexpr size_t C_KEY_BYTE = 128;                  // u64 argmax key
 // Exchange buffers of one layer; each region starts on a 256-byte boundary.
 constexpr size_t X_QKV = 0;                                 // bf16 q[2048] | k[512] | v[512]
@@ -837,12 +838,14 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     *kp = 0ull;
   }
   if (p.noalloc) {
-    // The static scratch has no reader for error bits: a faulted step reports
-    // next_token = -1 (and does not advance), and the bits are cleared so the
-    // next step's waits do not bail out.
+    // In the static scratch the step's error bits are cleared so the next
+    // step's waits do not bail out; a faulted step reports next_token = -1
+    // (if given), does not advance, and ORs its bits into the sticky word that
+    // mk_read_device_error(NULL, ...) returns and clears.
     const uint32_t bits = __hip_atomic_load(ctrl + C_ERR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ctrl[C_ERR] = 0u;
     if (bits) {
+      __hip_atomic_fetch_or(ctrl + C_STICKY, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (p.next_token) p.next_token[0] = -1;
       return;
     }
@@ -1241,11 +1244,30 @@ int mk_workspace_release(void* workspace) {
 }
 
 int mk_read_device_error(void* workspace, void* stream, uint32_t* bits_out) {
-  if (!workspace || !bits_out) return fail(MK_ERR_NULL, "workspace or bits_out is NULL");
+  if (!bits_out) return fail(MK_ERR_NULL, "bits_out is NULL");
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = hipStreamSynchronize(st);
   if (e != hipSuccess) return fail(MK_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
-  uint32_t* dev_err = reinterpret_cast<uint32_t*>(workspace) + C_ERR;
+  uint32_t* dev_err = nullptr;
+  if (workspace) {
+    dev_err = reinterpret_cast<uint32_t*>(workspace) + C_ERR;
+  } else {
+    // the allocation-free scratch of the current device (its address from
+    // hipGetSymbolAddress; nothing to read before its first use)
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
+    if (dev < 0 || dev >= 64) return fail(MK_ERR_DEVICE, "device index %d out of range", dev);
+    uint8_t* base = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(g_noalloc_mu);
+      base = g_noalloc[dev].ptr;
+    }
+    if (!base) {
+      *bits_out = 0u;
+      return MK_OK;
+    }
+    dev_err = reinterpret_cast<uint32_t*>(base) + C_STICKY;
+  }
   uint32_t bits = 0, zero = 0;
   e = hipMemcpy(&bits, dev_err, 4, hipMemcpyDeviceToHost);
   if (e == hipSuccess) e = hipMemcpy(dev_err, &zero, 4, hipMemcpyHostToDevice);

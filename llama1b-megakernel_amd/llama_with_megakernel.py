@@ -33,6 +33,7 @@ TP must be 1, as the reference asserts (llama_with_megakernel.py:147-150).
 from __future__ import annotations
 
 import dataclasses
+import weakref
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -76,6 +77,90 @@ class LlamaInferenceConfig:
     dims: LlamaDims = LLAMA_3_2_1B
 
 
+class NeuronLlamaDecoderLayerMK:
+    """The layer seam (NeuronLlamaDecoderLayerMK, llama_with_megakernel.py:65-204).
+
+    ``forward(hidden_states, attention_mask, position_ids, past_key_value,
+    adapter_ids, rotary_position_ids, residual, **kwargs) -> (hidden, (K, V),
+    cos, sin, residual)``:
+
+    * token generation (``past_key_value`` given), layer 0: one launch of the
+      megakernel runs all 16 layers (``transformer_llama_megakernel_16layers``)
+      over the parent model's caches; the result and every layer's present
+      (K, V) are stashed on the parent; cos / sin are the step's RoPE rows
+      (bf16 [1, 1, 64] each);
+    * token generation, layers 1..15: the stashed hidden state and this
+      layer's own (K, V), so a caller that aliases each layer's cache back
+      (NxDI in the reference) finds the same tensors;
+    * context encoding (no ``past_key_value``): this layer alone over the
+      prompt tokens, one single-layer step (``transformer_llama_megakernel_1layer``)
+      per token in position order, each writing its K/V row before the next
+      token attends to it. The reference runs its baseline layer here; the
+      model-level ``NeuronLlamaForCausalLM.prefill`` is the fast path.
+
+    Batch 1, TP=1 and the packed stack shapes are asserted as the reference
+    asserts its own (llama_with_megakernel.py:145-162).
+    """
+
+    def __init__(self, config: "LlamaInferenceConfig", layer_idx: int):
+        self.config = config
+        self.layer_idx = layer_idx
+        self._parent_model_ref = None        # set by the model's load()
+
+    @property
+    def _parent_model(self):
+        return self._parent_model_ref() if self._parent_model_ref is not None else None
+
+    def _check(self, parent) -> None:
+        d, nc = self.config.dims, self.config.neuron_config
+        assert nc.tp_degree == 1, f"megakernel is TP=1 only, got tp_degree={nc.tp_degree}"
+        L, H = d.n_layers, d.hidden
+        qkv = (d.n_q_heads + 2 * d.n_kv_heads) * d.head_dim
+        shapes = {"w_qkv": (L, qkv, H), "w_o": (L, H, d.n_q_heads * d.head_dim),
+                  "w_gu": (L, 2 * d.intermediate, H), "w_down": (L, H, d.intermediate)}
+        for k, want in shapes.items():
+            assert tuple(parent.packed[k].shape) == want, f"{k}.shape={tuple(parent.packed[k].shape)}, want {want}"
+        assert parent.batch_size == 1, "the layer seam runs batch 1 (the reference's [1, 8, S, 64] caches)"
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None, past_key_value=None,
+                adapter_ids=None, rotary_position_ids=None, residual=None, **kwargs):
+        parent = self._parent_model
+        assert parent is not None, "layers need _parent_model_ref, set by NeuronLlamaForCausalLM.load()"
+        import transformer_llama as tl
+        p = parent.packed
+        if past_key_value is not None and self.layer_idx == 0:
+            self._check(parent)
+            K, V = parent.k_caches, parent.v_caches
+            pos = position_ids.reshape(-1)[:1].to(device=hidden_states.device, dtype=torch.int32)
+            out = tl.transformer_llama_megakernel_16layers(
+                hidden_states.to(torch.bfloat16), p["w_qkv"], p["w_o"], p["w_gu"], p["w_down"], *K, *V,
+                p["rope"], pos)
+            L = len(K)
+            Y, present = out[0], [(out[1 + i], out[1 + L + i]) for i in range(L)]
+            row = p["rope"][pos.long()].reshape(1, 1, -1)
+            half = row.shape[-1] // 2
+            parent._mk_outputs = {"hidden_states": Y, "present_kv": present}
+            return Y, present[0], row[..., :half], row[..., half:], None
+        if past_key_value is not None:
+            st = parent._mk_outputs
+            return st["hidden_states"], st["present_kv"][self.layer_idx], None, None, None
+        # context encoding: this layer over the prompt, token by token
+        self._check(parent)
+        l = self.layer_idx
+        X = hidden_states.reshape(-1, self.config.dims.hidden).to(torch.bfloat16)
+        pos = position_ids.reshape(-1).to(device=X.device, dtype=torch.int32)
+        if pos.numel() != X.shape[0]:
+            raise ValueError(f"{pos.numel()} positions for {X.shape[0]} tokens")
+        K, V = parent.k_caches[l], parent.v_caches[l]
+        rows = [tl.transformer_llama_megakernel_1layer(X[t], p["w_qkv"], p["w_o"], p["w_gu"], p["w_down"], K, V,
+                                                      p["rope"], pos[t:t + 1], layer=l)[0]
+                for t in range(X.shape[0])]
+        Y = torch.cat(rows, 1)                  # [1, n, H]
+        return Y, (K, V), None, None, None
+
+    __call__ = forward
+
+
 class NeuronLlamaForCausalLMMK:
     """Llama-3.2-1B whose token-generation step is one megakernel launch."""
 
@@ -109,15 +194,54 @@ class NeuronLlamaForCausalLMMK:
             return synthetic_state_dict(seed=int(self.model_path.split(":", 1)[1] or 0), d=self.config.dims)
         return load_hf_checkpoint(self.model_path, self.config.dims)
 
+    MANIFEST = "mk_compiled.json"
+
+    def manifest(self) -> dict:
+        """What a compiled model consists of in this build: the kernel library
+        (compiled ahead of time) and the weights it packs at load."""
+        import hashlib
+        nc = self.neuron_config
+        return {"abi_version": mk_lib.ABI_VERSION,
+                "libmk_sha256": hashlib.sha256(mk_lib.LIB_PATH.read_bytes()).hexdigest(),
+                "model_path": self.model_path, "dims": dataclasses.asdict(self.config.dims),
+                "batch_size": nc.batch_size, "seq_len": nc.seq_len, "max_context_length": nc.max_context_length,
+                "dtype": "bfloat16", "tp_degree": nc.tp_degree}
+
     def compile(self, compiled_model_path: Optional[str] = None, debug: bool = False) -> None:
-        """Pack the weights onto the device (the reference traces and compiles
-        a NEFF here; the HIP kernel is compiled ahead of time into libmk.so)."""
+        """Pack the weights onto the device. The reference traces and compiles
+        a NEFF into ``compiled_model_path`` here (main.py:143); this build's
+        kernel is compiled ahead of time into libmk.so, so the directory, when
+        given, receives a manifest (library hash, ABI version, weights source,
+        shapes) that ``load`` checks."""
         mk_lib.load()   # fails loudly if the native library is missing
         sd = self.load_state_dict_source()
         self.state_dict_bf16 = sd
         self.packed = self.convert_hf_to_neuron_state_dict(sd, self.config, device=self.neuron_config.device)
+        if compiled_model_path:
+            import json
+            from pathlib import Path
+            out = Path(compiled_model_path)
+            out.mkdir(parents=True, exist_ok=True)
+            (out / self.MANIFEST).write_text(json.dumps(self.manifest(), indent=1, sort_keys=True))
+
+    def check_manifest(self, compiled_model_path: str) -> None:
+        import json
+        from pathlib import Path
+        f = Path(compiled_model_path) / self.MANIFEST
+        if not f.exists():
+            raise FileNotFoundError(f"{f} is missing: call compile({compiled_model_path!r}) first")
+        got, want = json.loads(f.read_text()), self.manifest()
+        diff = sorted(k for k in want if got.get(k) != want[k])
+        if diff:
+            raise ValueError(f"{f} was compiled for another model or library (differs in {diff}): compile again")
 
     def load(self, compiled_model_path: Optional[str] = None) -> None:
+        """Allocate the caches and workspaces (main.py:150). With a
+        ``compiled_model_path`` its manifest must describe this model and
+        library; a missing or stale one is an error, as loading a NEFF traced
+        for other shapes would be."""
+        if compiled_model_path:
+            self.check_manifest(compiled_model_path)
         if self.packed is None:
             self.compile(compiled_model_path)
         nc, d = self.neuron_config, self.config.dims
@@ -145,6 +269,12 @@ class NeuronLlamaForCausalLMMK:
         self.pf_pos = torch.arange(self.s_max, dtype=torch.int32, device=dev)
         self._ready = True
         self._launchers: Dict[str, mk_lib.StepLauncher] = {}
+        # the layer seam (NeuronLlamaModelMK.init_model installs the same parent weakrefs,
+        # llama_with_megakernel.py:210-250)
+        self.layers = [NeuronLlamaDecoderLayerMK(self.config, i) for i in range(d.n_layers)]
+        for layer in self.layers:
+            layer._parent_model_ref = weakref.ref(self)
+        self._mk_outputs: Optional[dict] = None
 
     def reset(self) -> None:
         """Start new sequences (rows >= pos are never read, so no cache clear)."""
@@ -208,6 +338,24 @@ class NeuronLlamaForCausalLMMK:
         mk_lib.decode_step(self.weights, self.ws, ks, vs, pos, tokens=toks, hidden_in=hid,
                            logits=self.logits[:nb], next_token=self.tokens[:nb], batch=nb)
         return self.logits[:nb], kv
+
+    @torch.no_grad()
+    def layer_stack_forward(self, hidden_states: torch.Tensor, position_ids: torch.Tensor,
+                            past_key_values: Optional[Sequence[Tuple[torch.Tensor, torch.Tensor]]] = None):
+        """The decoder-layer loop of NxDI's model forward over the layer seam:
+        each layer called with (hidden, position_ids, its past_key_value), the
+        returned hidden state fed to the next. Token generation passes the
+        caches (the megakernel runs in layer 0); context encoding passes
+        ``past_key_values=None`` with the prompt's hidden states [1, n, H] and
+        positions [1, n]. Returns the hidden state after the last layer (before
+        the final norm) and the per-layer present (K, V)."""
+        assert self._ready, "call load() first"
+        h, present = hidden_states, []
+        for i, layer in enumerate(self.layers):
+            kv = None if past_key_values is None else past_key_values[i]
+            h, kv_out, _, _, _ = layer(h, position_ids=position_ids, past_key_value=kv)
+            present.append(kv_out)
+        return h, present
 
     def _prompts(self, input_ids) -> List[torch.Tensor]:
         """The batch's prompts as 1-D tensors: [n] (batch 1), [B, n], or a list
@@ -315,6 +463,7 @@ class NeuronLlamaForCausalLMMK:
                     mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
                 self.graph_tokens[i].copy_(self.tokens)
         graph._mk_keep = (step, sampling_params, stream)
+        self.ws.register_graph(graph)            # the workspace is not released while the graph lives
         return graph
 
     @torch.no_grad()

@@ -25,7 +25,7 @@ prompt as token ids instead (repeatable); with no prompt at all,
   teacher forcing after a divergence as in check_accuracy_logits
   (main.py:274-357): per-step logit error and greedy agreement; the criteria
   are those of tests/test_gpu_decode.py (bf16 noise floor, see there). The
-  reference's tol_map and divergence tolerance (main.py:51, 542) are reported
+  reference's tol_map and divergence tolerance (main.py:51, 544) are reported
   as restated checks (mk_validate).
 * benchmark: e2e / context-encoding / token-generation latency percentiles and
   throughput in the shape of NxDI's benchmark report (main.py:178-271),
@@ -54,36 +54,181 @@ sys.path.insert(0, str(Path(__file__).resolve().parent))
 BENCHMARK_REPORT_FILENAME = "benchmark_report.json"
 
 
+def _torch_dtype(name: str) -> torch.dtype:
+    """The reference parses --torch-dtype / --rpl-reduce-dtype with NxDI's
+    to_torch_dtype (main.py:66, 75): a dtype name such as "bfloat16"."""
+    key = str(name).lower().replace("torch.", "")
+    table = {"bfloat16": torch.bfloat16, "bf16": torch.bfloat16, "float16": torch.float16, "fp16": torch.float16,
+             "half": torch.float16, "float32": torch.float32, "fp32": torch.float32, "float": torch.float32,
+             "float64": torch.float64, "double": torch.float64}
+    if key not in table:
+        raise argparse.ArgumentTypeError(f"unknown torch dtype {name!r}")
+    return table[key]
+
+
+def _flag_bool(v) -> bool:
+    """--do-sample / --enable-bucketing take a value as in the reference
+    (main.py:62, 89). The reference's ``type=bool`` reads any non-empty string,
+    "False" included, as True; here "0", "false" and "no" read as False."""
+    return str(v).lower() in ("1", "true", "yes", "y", "on")
+
+
 def parse_args(argv=None):
+    """Every flag of the reference's parser (main.py:34-105), plus this build's
+    own (benchmark mode, --prompt-ids, --prompt-len, --tokenizer-path, --seed,
+    --graph, --num-runs, --report-path). Flags for Neuron features this build
+    has no counterpart for are accepted; a value this build cannot honour is
+    refused by check_args with a message naming the flag."""
     ap = argparse.ArgumentParser()
-    ap.add_argument("--mode", choices=["generate", "validate", "benchmark"], required=True)
-    ap.add_argument("--enable-nki", action="store_true")
-    ap.add_argument("--model-path", default="random:0")
-    ap.add_argument("--tokenizer-path", default=None,
-                    help="local tokenizer directory (default: --model-path when it is a directory)")
+    # ASPLOS contest specific (main.py:37-41)
+    ap.add_argument("--mode", choices=["generate", "validate", "benchmark", "evaluate_single", "evaluate_all"],
+                    required=True)
+    ap.add_argument("--llama", type=str, default="llama",
+                    help="model module: llama (the stock path, or the megakernel with --enable-nki) "
+                         "or llama_with_megakernel")
+    ap.add_argument("--enable-nki", action="store_true", help="run the megakernel model (llama_with_megakernel)")
+    ap.add_argument("--base-latency", type=float, default=526.15, help="contest scoring only (evaluate_*)")
+    ap.add_argument("--base-throughput", type=float, default=134.61, help="contest scoring only (evaluate_*)")
+    # Model path (main.py:44-47)
+    ap.add_argument("--model-path", default="random:0",
+                    help="local HF checkpoint directory (safetensors) or random:<seed>")
+    ap.add_argument("--compiled-model-path", default=None,
+                    help="directory for the compiled-model manifest and the tokenizer (the reference writes its "
+                         "traced NEFF there)")
+    # Evaluation (main.py:49-53)
+    ap.add_argument("--benchmark", action="store_true", help="accepted (a NeuronConfig field; no effect in main.py)")
+    ap.add_argument("--divergence-difference-tol", type=float, default=None,
+                    help="validate: logit gap under which a greedy divergence is a tie (default 0.001)")
+    ap.add_argument("--tol-map", type=str, default=None,
+                    help="validate: {top_k: (atol, rtol)} as a Python literal (default: the reference's, main.py:544)")
+    ap.add_argument("--num-tokens-to-check", type=int, default=None)
+    # Generation (main.py:55-63)
     ap.add_argument("--prompt", dest="prompts", action="append", default=None, help="text prompt (repeatable)")
     ap.add_argument("--prompt-ids", action="append", default=None,
                     help="comma-separated token ids of one prompt (repeatable)")
     ap.add_argument("--prompt-len", type=int, default=384, help="random prompt length (seed 0) if no prompt")
-    ap.add_argument("--max-new-tokens", type=int, default=640)
-    ap.add_argument("--seq-len", type=int, default=1024)
-    ap.add_argument("--max-context-length", type=int, default=None)
-    ap.add_argument("--batch-size", type=int, default=1, help="random prompts drawn when no prompt is given")
-    ap.add_argument("--tp-degree", type=int, default=1)
+    ap.add_argument("--tokenizer-path", default=None,
+                    help="local tokenizer directory (default: --model-path when it is a directory)")
     ap.add_argument("--top-k", type=int, default=1)
     ap.add_argument("--top-p", type=float, default=1.0)
     ap.add_argument("--temperature", type=float, default=1.0)
     ap.add_argument("--global-topk", type=int, default=None,
                     help="candidate cap of the on-device sampler (at most 1024, the built-in cap)")
-    ap.add_argument("--do-sample", type=lambda v: str(v).lower() in ("1", "true", "yes"), default=True)
+    ap.add_argument("--do-sample", type=_flag_bool, default=True)
+    ap.add_argument("--dynamic", action="store_true", help="accepted (a generation-config field; no effect here)")
+    ap.add_argument("--pad-token-id", type=int, default=2,
+                    help="accepted: prompts are not padded here (each sequence keeps its own length)")
+    ap.add_argument("--seed", type=int, default=0, help="Philox key of the on-device sampler")
+    # Basic config (main.py:65-77)
+    ap.add_argument("--torch-dtype", type=_torch_dtype, default=torch.bfloat16)
+    ap.add_argument("--batch-size", type=int, default=1, help="random prompts drawn when no prompt is given")
+    ap.add_argument("--padding-side", type=str, default=None, choices=[None, "left", "right"],
+                    help="tokenizer padding side (prompts are not padded here)")
+    ap.add_argument("--seq-len", type=int, default=1024,
+                    help="cache rows per sequence = max_length (the reference's default 64 fails its own "
+                         "megakernel's asserts, llama_with_megakernel.py:159-162)")
+    ap.add_argument("--n-active-tokens", type=int, default=None, help="accepted (NxDI tracing shape)")
+    ap.add_argument("--n-positions", type=int, default=None, help="positions of the model; must be >= --seq-len")
+    ap.add_argument("--max-context-length", type=int, default=None)
+    ap.add_argument("--max-new-tokens", type=int, default=None,
+                    help="default: up to --seq-len (seq_len minus the longest prompt, as the reference's max_length)")
+    ap.add_argument("--max-length", type=int, default=None,
+                    help="accepted; set to --seq-len as the reference does (main.py:543)")
+    ap.add_argument("--rpl-reduce-dtype", type=_torch_dtype, default=None,
+                    help="accepted: the TP all-reduce dtype; TP=1 has no all-reduce")
+    ap.add_argument("--output-logits", action="store_true",
+                    help="generate: also return the per-step logits and print their summary")
+    ap.add_argument("--vocab-parallel", action="store_true", help="accepted: no vocabulary split at TP=1")
+    # Attention (main.py:79-82)
+    ap.add_argument("--fused-qkv", action="store_true", help="accepted: Q, K and V are always one fused GEMV")
+    ap.add_argument("--sequence-parallel-enabled", action="store_true", help="accepted: no sequence split at TP=1")
+    ap.add_argument("--flash-decoding-enabled", action="store_true",
+                    help="accepted: decode attention is always split over the KV length")
+    # On device sampling (main.py:84-85)
     ap.add_argument("--on-device-sampling", action="store_true",
                     help="accepted for the reference's CLI; sampling always runs on the GPU here")
-    ap.add_argument("--seed", type=int, default=0, help="Philox key of the on-device sampler")
+    # Bucketing (main.py:87-91)
+    ap.add_argument("--enable-bucketing", type=_flag_bool, default=True,
+                    help="accepted: no traced buckets (every length runs the same kernel)")
+    ap.add_argument("--bucket-n-active-tokens", action="store_true", help="accepted (no traced buckets)")
+    ap.add_argument("--context-encoding-buckets", nargs="+", type=int, default=None,
+                    help="accepted; each bucket must fit --seq-len")
+    ap.add_argument("--token-generation-buckets", nargs="+", type=int, default=None,
+                    help="accepted; each bucket must fit --seq-len")
+    # Parallelism (main.py:93-94)
+    ap.add_argument("--tp-degree", type=int, default=1,
+                    help="must be 1 (llama_with_megakernel.py:147-150; the reference's default 2 fails there)")
+    # Kernels (main.py:96-103)
+    ap.add_argument("--qkv-kernel-enabled", action="store_true", help="accepted: the megakernel fuses QKV")
+    ap.add_argument("--attn-kernel-enabled", action="store_true", help="accepted: the megakernel fuses attention")
+    ap.add_argument("--mlp-kernel-enabled", action="store_true", help="accepted: the megakernel fuses the MLP")
+    ap.add_argument("--quantized-mlp-kernel-enabled", action="store_true",
+                    help="refused: this build computes in bf16 only")
+    ap.add_argument("--rmsnorm-quantize-kernel-enabled", action="store_true",
+                    help="refused: this build computes in bf16 only")
+    ap.add_argument("--quantized-kernel-lower-bound", type=float, default=1200.0,
+                    help="accepted (used only with the quantized MLP kernel)")
+    ap.add_argument("--mlp-kernel-fuse-residual-add", action="store_true",
+                    help="accepted: the residual add is always fused")
+    # this build's benchmark mode
     ap.add_argument("--graph", action="store_true", help="benchmark: replay the decode steps as one HIP graph")
     ap.add_argument("--num-runs", type=int, default=5)
-    ap.add_argument("--num-tokens-to-check", type=int, default=None)
     ap.add_argument("--report-path", default=BENCHMARK_REPORT_FILENAME)
-    return ap.parse_args(argv)
+    args = ap.parse_args(argv)
+    check_args(args)
+    return args
+
+
+MODULES = ("llama", "llama_with_megakernel")
+
+
+def check_args(args) -> None:
+    """Refuse values this build cannot honour, with the flag named (the
+    reference's own asserts, llama_with_megakernel.py:145-162, plus this
+    build's bf16-only kernels)."""
+    if args.mode in ("evaluate_single", "evaluate_all"):
+        raise SystemExit(f"--mode {args.mode} scores the reference's ASPLOS contest (trn1 baselines, the NKI "
+                         "share of the traced HLO, prompts.txt with a real checkpoint; main.py:586-669): out of "
+                         "scope for this build. Use --mode validate for accuracy and --mode benchmark for latency.")
+    if args.llama not in MODULES:
+        raise SystemExit(f"--llama {args.llama!r}: this build has the modules {', '.join(MODULES)}")
+    if args.llama == "llama_with_megakernel":
+        args.enable_nki = True
+    if args.torch_dtype != torch.bfloat16:
+        raise SystemExit(f"--torch-dtype {args.torch_dtype}: the megakernel computes in bfloat16 only")
+    if args.quantized_mlp_kernel_enabled or args.rmsnorm_quantize_kernel_enabled:
+        raise SystemExit("--quantized-mlp-kernel-enabled / --rmsnorm-quantize-kernel-enabled: "
+                         "this build computes in bfloat16 only (no quantized kernels)")
+    if args.tp_degree != 1:
+        raise SystemExit(f"--tp-degree {args.tp_degree}: the megakernel is TP=1 only "
+                         "(llama_with_megakernel.py:147-150)")
+    if args.n_positions is not None and args.n_positions < args.seq_len:
+        raise SystemExit(f"--n-positions {args.n_positions} < --seq-len {args.seq_len}")
+    for name in ("context_encoding_buckets", "token_generation_buckets"):
+        for b in getattr(args, name) or []:
+            if not 1 <= b <= args.seq_len:
+                raise SystemExit(f"--{name.replace('_', '-')} {b}: buckets must lie in [1, --seq-len]")
+    if args.max_new_tokens is not None and args.max_new_tokens < 1:
+        raise SystemExit("--max-new-tokens must be >= 1")
+    if args.divergence_difference_tol is not None and args.divergence_difference_tol < 0:
+        raise SystemExit("--divergence-difference-tol must be >= 0")
+    args.max_length = args.seq_len             # main.py:543
+    from mk_validate import parse_tol_map
+    try:
+        args.tol_map_parsed = parse_tol_map(args.tol_map)
+    except ValueError as e:
+        raise SystemExit(f"--tol-map: {e}")
+
+
+def max_new_tokens(args, prompts) -> int:
+    """--max-new-tokens, or what fills --seq-len after the longest prompt (the
+    reference generates up to max_length = seq_len, main.py:543)."""
+    if args.max_new_tokens is not None:
+        return args.max_new_tokens
+    n = args.seq_len - max(int(p.numel()) for p in prompts) + 1
+    if n < 1:
+        raise SystemExit(f"a prompt of {max(int(p.numel()) for p in prompts)} tokens fills --seq-len {args.seq_len}")
+    return n
 
 
 def tokenizer_dir(args) -> Optional[str]:
@@ -94,14 +239,28 @@ def tokenizer_dir(args) -> Optional[str]:
     return None
 
 
-def load_tokenizer(path: str):
+def load_tokenizer(path: str, padding_side: Optional[str] = None, compiled_model_path: Optional[str] = None):
     """The checkpoint's tokenizer from a local directory (main.py:114-118):
-    no network, pad token = EOS."""
+    no network, pad token = EOS, a copy saved into the compiled-model
+    directory when one is given (as the reference does)."""
     from transformers import AutoTokenizer
-    tok = AutoTokenizer.from_pretrained(path, local_files_only=True)
+    kw = {"padding_side": padding_side} if padding_side else {}
+    tok = AutoTokenizer.from_pretrained(path, local_files_only=True, **kw)
     if tok.pad_token is None:
         tok.pad_token = tok.eos_token
+    if compiled_model_path:
+        tok.save_pretrained(compiled_model_path)
     return tok
+
+
+def args_tokenizer(args):
+    """The tokenizer main.py's modes use, or None (random weights, no
+    tokenizer directory)."""
+    d = tokenizer_dir(args)
+    return load_tokenizer(d, args.padding_side, args.compiled_model_path) if d else None
+
+
+REFERENCE_DEFAULT_PROMPT = "I believe the meaning of life is"     # main.py:538-539
 
 
 def encode_prompts(args, tokenizer=None) -> List[torch.Tensor]:
@@ -112,7 +271,7 @@ def encode_prompts(args, tokenizer=None) -> List[torch.Tensor]:
             d = tokenizer_dir(args)
             if d is None:
                 raise SystemExit("--prompt needs a tokenizer: give --tokenizer-path (a local directory)")
-            tokenizer = load_tokenizer(d)
+            tokenizer = load_tokenizer(d, args.padding_side)
         for text in args.prompts:
             ids = tokenizer(text)["input_ids"]
             if not ids:
@@ -120,6 +279,9 @@ def encode_prompts(args, tokenizer=None) -> List[torch.Tensor]:
             prompts.append(torch.tensor(ids, dtype=torch.int64))
     for s in args.prompt_ids or []:
         prompts.append(torch.tensor([int(x) for x in s.split(",")], dtype=torch.int64))
+    if not prompts and tokenizer is not None:
+        ids = tokenizer(REFERENCE_DEFAULT_PROMPT)["input_ids"]
+        prompts = [torch.tensor(ids, dtype=torch.int64)]
     if not prompts:
         from mk_weights import random_token_ids
         prompts = [random_token_ids(args.prompt_len, seed=b) for b in range(args.batch_size)]
@@ -150,8 +312,8 @@ def prepare_inference(args, batch: int):
                              tp_degree=args.tp_degree)
     model = NeuronLlamaForCausalLM(args.model_path, LlamaInferenceConfig(nc))
     t0 = time.monotonic()
-    model.compile()
-    model.load()
+    model.compile(args.compiled_model_path)
+    model.load(args.compiled_model_path)
     print(f"model ready in {time.monotonic() - t0:.1f}s (weights packed on the GPU), batch {batch}", flush=True)
     return model
 
@@ -164,13 +326,19 @@ def _state_dict(args):
 
 
 def run_generation(args):
-    d = tokenizer_dir(args)
-    tokenizer = load_tokenizer(d) if d else None
+    tokenizer = args_tokenizer(args)
     prompts = encode_prompts(args, tokenizer)
     B = len(prompts)
+    n_new = max_new_tokens(args, prompts)
+    lg = None
     if args.enable_nki:
         model = prepare_inference(args, B)
-        out = model.generate(prompts, args.max_new_tokens, sampling_params=sampling_params(args, B), seed=args.seed)
+        out = model.generate(prompts, n_new, sampling_params=sampling_params(args, B), seed=args.seed,
+                             return_logits=args.output_logits)
+        if args.output_logits:
+            out, lg = out
+            if lg.dim() == 2:
+                lg = lg[None]
     else:
         if sampling_params(args) is not None:
             raise SystemExit("the stock path decodes greedily; sampling needs --enable-nki")
@@ -181,29 +349,50 @@ def run_generation(args):
             for p in range(len(ids) - 1):
                 base.step(int(ids[p]), p)
             tok, row = int(ids[-1]), []
-            for t in range(args.max_new_tokens):
-                tok = int(base.step(tok, len(ids) - 1 + t).argmax())
+            lrow = []
+            for t in range(n_new):
+                step = base.step(tok, len(ids) - 1 + t).float().cpu()
+                tok = int(step.argmax())
                 row.append(tok)
+                if args.output_logits:
+                    lrow.append(step)
             rows.append(row)
+            if args.output_logits:
+                lg = (lg or []) + [torch.stack(lrow)]
         out = torch.tensor(rows)
+        if args.output_logits:
+            lg = torch.stack(lg)
+    if out.dim() == 1:
+        out = out[None]
     for b in range(B):
         print(f"Output {b}: token ids {out[b].tolist()}")
+        if lg is not None:
+            print(f"Output {b}: logits [{lg.shape[1]}, {lg.shape[2]}] fp32; per-step max "
+                  f"{[round(float(x), 3) for x in lg[b].max(-1).values]}")
         if tokenizer is not None:
             print(f"Output {b}: {tokenizer.decode(out[b].tolist(), skip_special_tokens=True)!r}")
     return out
 
 
 def run_accuracy_check(args) -> bool:
+    """The reference's validate mode (check_accuracy_logits, main.py:274-357)
+    for this build: the megakernel model's greedy generation, teacher-forced
+    through the stock fp32 path on the same weights, compared step by step.
+    Pass rule: validate_pass; the reference's tol_map / divergence tolerance
+    (--tol-map, --divergence-difference-tol) are reported as restated checks."""
     from llama_baseline import StockLlama
     from mk_validate import REFERENCE_DIVERGENCE_TOL, divergences, topk_tolerance
-    d = tokenizer_dir(args)
-    prompts = encode_prompts(args, load_tokenizer(d) if d else None)
+    tokenizer = args_tokenizer(args)
+    prompts = encode_prompts(args, tokenizer)
     model = prepare_inference(args, len(prompts))
-    toks, logits = model.generate(prompts, args.max_new_tokens, return_logits=True)   # [B, T], [B, T, V]
-    n_check = args.num_tokens_to_check or args.max_new_tokens
+    n_new = max_new_tokens(args, prompts)
+    toks, logits = model.generate(prompts, n_new, return_logits=True)   # [B, T], [B, T, V]
+    n_check = min(args.num_tokens_to_check or n_new, n_new)
+    if args.num_tokens_to_check is not None:
+        print(f"Validating logits for first {n_check} tokens")
     base = StockLlama(model.state_dict_bf16, s_max=model.s_max)
-    agree, decided, decided_ok, worst, worst_rms, first_div = 0, 0, 0, 0.0, 0.0, None
-    got_all, refs_all = [], []
+    worst, worst_rms, first_div = 0.0, 0.0, None
+    got_all, refs_all, agree, gaps = [], [], [], []
     for b, ids in enumerate(prompts):
         seq = torch.cat([ids, toks[b].long()])
         for p in range(len(ids) - 1):
@@ -216,47 +405,58 @@ def run_accuracy_check(args) -> bool:
             worst = max(worst, dd.max().item())
             worst_rms = max(worst_rms, dd.pow(2).mean().sqrt().item())
             same = int(ref.argmax()) == int(toks[b, t])
-            agree += same
             if not same and first_div is None:
                 first_div = (b, t)
             top2 = ref.topk(2).values
-            if float(top2[0] - top2[1]) >= 0.1:
-                decided += 1
-                decided_ok += same
-    n_all = n_check * len(prompts)
-    rate = agree / n_all
-    rate_dec = decided_ok / max(decided, 1)
-    floor = overall_agreement_floor(n_all)
+            agree.append(same)
+            gaps.append(float(top2[0] - top2[1]))
+    ok, st = validate_pass(agree, gaps, worst, worst_rms)
     print(f"validate: {len(prompts)} sequence(s) x {n_check} tokens, teacher-forced greedy agreement "
-          f"{rate * 100:.2f}% (floor {floor * 100:.1f}%) (where the baseline's top-2 gap >= 0.1: "
-          f"{rate_dec * 100:.2f}% of {decided}); first divergence at (sequence, step) {first_div}; "
+          f"{st['all'] * 100:.2f}%; where the baseline's top-2 gap >= {CLEAR_GAP}: {st['clear'] * 100:.2f}% of "
+          f"{st['n_clear']} (floor {CLEAR_FLOOR * 100:.0f}%); where >= {DECIDED_GAP}: {st['decided'] * 100:.2f}% of "
+          f"{st['n_decided']} (floor {DECIDED_FLOOR * 100:.0f}%); first divergence at (sequence, step) {first_div}; "
           f"logits max|d| {worst:.3e}, worst per-step rms {worst_rms:.3e}")
-    # the reference's logit_validation parameters (main.py:51, 542) as restated checks; reported,
+    # the reference's logit_validation parameters (main.py:51, 544) as restated checks; reported,
     # not part of the pass rule (their rtol on near-zero logits is below the bf16 noise floor)
     got_all, refs_all = torch.stack(got_all), torch.stack(refs_all)
-    tm = topk_tolerance(got_all, refs_all)
-    dv = divergences(got_all, refs_all, REFERENCE_DIVERGENCE_TOL)
-    print("validate: reference tol_map (restated; steps passing / worst ratio): " +
+    tol = REFERENCE_DIVERGENCE_TOL if args.divergence_difference_tol is None else args.divergence_difference_tol
+    tm = topk_tolerance(got_all, refs_all, args.tol_map_parsed)
+    dv = divergences(got_all, refs_all, tol)
+    print("validate: tol_map (restated; steps passing / worst ratio): " +
           ", ".join(f"{k} {v['steps_passing'] * 100:.1f}% / {v['worst_ratio']:.2f}" for k, v in tm.items()) +
-          f"; greedy divergences {dv['steps']}, {dv['within_tol']} within {REFERENCE_DIVERGENCE_TOL}")
-    return worst <= 0.2 and worst_rms <= 0.03 and rate_dec >= 0.99 and rate >= floor
+          f"; greedy divergences {dv['steps']}, {dv['within_tol']} within divergence_difference_tol {tol}")
+    return ok
 
 
-# Greedy agreement of two bf16 implementations over all positions is bounded by
-# near-ties: with random-init weights the CPU reference agrees with its own
-# fp64-accumulation variant on 93.1% of 640 teacher-forced positions. The
-# overall floor is 90%, or three binomial standard deviations below 93.1% for
-# short runs where fewer positions make the rate noisier. (Each change of a
-# kernel's accumulation order draws a new sample of which near-ties flip; at two
-# deviations about one such change in 40 fails a correct kernel, as a 48-token
-# run did with 41/48 agreeing and every position with a top-2 gap >= 0.1 equal.)
-AGREEMENT_NOISE_FLOOR = 0.931
-AGREEMENT_FLOOR_SIGMAS = 3.0
+# Validate pass rule. Two correct bf16 implementations of the step disagree on
+# the greedy token wherever the top-2 logits are closer than their rounding
+# noise (per-step logit rms ~0.02): with random-init weights the CPU oracle and
+# its own fp64-accumulation variant disagree on 44 of the 640 config-3
+# positions, all with a top-2 gap below 0.1, and those flips cluster along the
+# trajectory (tests/golden/c3_self_agreement.json). A floor on the agreement
+# over ALL positions therefore fails correct runs: 28 of the 593 48-position
+# windows of that fixture fall below even a floor three binomial deviations
+# under the mean. Near-ties are excluded instead: the agreement must be >= 90%
+# where the baseline's top-2 gap is >= 0.03 (every window of >= 24 positions of
+# the fixture passes) and >= 99% where it is >= 0.1 (100% in the fixture).
+CLEAR_GAP, CLEAR_FLOOR = 0.03, 0.90
+DECIDED_GAP, DECIDED_FLOOR = 0.1, 0.99
+MAX_ABS_BOUND, RMS_BOUND = 0.2, 0.03
 
 
-def overall_agreement_floor(n: int) -> float:
-    p = AGREEMENT_NOISE_FLOOR
-    return min(0.90, p - AGREEMENT_FLOOR_SIGMAS * (p * (1.0 - p) / max(n, 1)) ** 0.5)
+def validate_pass(agree, gaps, worst_max_abs: float = 0.0, worst_rms: float = 0.0):
+    """(passed, stats) of validate mode's rule for per-position greedy
+    agreement flags and the baseline's top-2 logit gaps at those positions."""
+    def rate(th):
+        sel = [a for a, g in zip(agree, gaps) if g >= th]
+        return (sum(sel) / len(sel) if sel else 1.0), len(sel)
+    clear, n_clear = rate(CLEAR_GAP)
+    decided, n_decided = rate(DECIDED_GAP)
+    st = {"all": sum(agree) / max(len(agree), 1), "clear": clear, "n_clear": n_clear, "decided": decided,
+          "n_decided": n_decided}
+    ok = (worst_max_abs <= MAX_ABS_BOUND and worst_rms <= RMS_BOUND and clear >= CLEAR_FLOOR
+          and decided >= DECIDED_FLOOR)
+    return ok, st
 
 
 def generate_report(latencies_ms: List[float], tokens: int) -> dict:
@@ -277,11 +477,10 @@ def benchmark_sampling(args):
     steps of a run replay one captured HIP graph (the per-step latency is then
     the run's generation time / steps)."""
     import mk_lib
-    d = tokenizer_dir(args)
-    prompts = encode_prompts(args, load_tokenizer(d) if d else None)
+    prompts = encode_prompts(args, args_tokenizer(args))
     B = len(prompts)
     model = prepare_inference(args, B)
-    n_new = args.max_new_tokens
+    n_new = max_new_tokens(args, prompts)
     sp = sampling_params(args, B)
     dec = model.launcher("decode" if sp is None else "decode_logits")
     graph = model.decode_graph(n_new, sampling_params=sp, seed=args.seed) if args.graph else None

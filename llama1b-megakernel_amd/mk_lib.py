@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import sys
+import weakref
 from ctypes import POINTER, c_char_p, c_int, c_int32, c_size_t, c_uint32, c_void_p
 from pathlib import Path
 from typing import Dict, List, Optional, Sequence
@@ -17,6 +18,7 @@ from typing import Dict, List, Optional, Sequence
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmk.so")
+ABI_VERSION = 1             # MK_ABI_VERSION of include/mk.h
 
 MK_OK = 0
 ERRORS = {
@@ -109,6 +111,9 @@ def load() -> ctypes.CDLL:
         lib.mk_sample.argtypes = [POINTER(MkSampleArgs)]
         lib.mk_sample.restype = c_int
         lib.mk_sample_last_error.restype = c_char_p
+        if lib.mk_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {lib.mk_abi_version()}, this module {ABI_VERSION}: "
+                               "rebuild it")
         _lib = lib
     return _lib
 
@@ -148,13 +153,43 @@ def weights_struct(packed: Dict[str, torch.Tensor], tiled: bool = True) -> MkWei
         int(packed["w_qkv"].shape[0]), int(packed["rope"].shape[0]), *t_ptrs)
 
 
+_deferred: List["_Released"] = []     # collected workspaces whose exchange area is not yet returned
+
+
+def _drain_deferred() -> None:
+    """Return the exchange areas of workspaces collected since the last call
+    (never from a finaliser: mk_workspace_release synchronises the device,
+    which is illegal while any stream captures a graph)."""
+    while _deferred:
+        ws = _deferred.pop()
+        try:
+            with torch.cuda.device(ws.device):
+                check(load().mk_workspace_release(ws.buf.data_ptr()))
+        except Exception:
+            pass
+
+
+class _Released:
+    """A collected workspace's device and buffer, kept until its area is returned."""
+
+    def __init__(self, device, buf):
+        self.device, self.buf = device, buf
+
+
 class Workspace:
-    """Device workspace for one stream of steps (initialised once at creation;
-    the library's exchange area for it is returned by ``release()``, which
-    also runs when the object is garbage-collected)."""
+    """Device workspace for one stream of steps (initialised once at creation).
+
+    Its exchange area in the library is returned by ``release()``, which
+    synchronises the device. A HIP graph that captured steps on this workspace
+    holds the area's address in its kernel arguments, so ``release()`` refuses
+    while a graph registered with ``register_graph`` is alive (a replay would
+    write freed memory), and it must not be called during a stream capture.
+    When the object is collected, its buffer and area are kept and returned by
+    the next ``Workspace`` created, outside any capture."""
 
     def __init__(self, batch: int, s_max: int, device: torch.device):
         lib = load()
+        _drain_deferred()
         n = lib.mk_workspace_bytes(batch, s_max)
         if n == 0:
             raise MkError(-4, f"no workspace size for batch={batch}, s_max={s_max}")
@@ -164,23 +199,35 @@ class Workspace:
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
         assert self.buf.data_ptr() % 256 == 0
         self._live = False
+        self._graphs = weakref.WeakSet()
         check(lib.mk_workspace_init(self.buf.data_ptr(), self.nbytes, c_void_p(current_stream_ptr())))
         self._live = True
+
+    def register_graph(self, graph) -> None:
+        """Record a graph that captured steps on this workspace: release()
+        refuses while it is alive."""
+        self._graphs.add(graph)
 
     def release(self) -> None:
         """mk_workspace_release: synchronises the device and returns the
         exchange area (the workspace is unusable afterwards)."""
-        if self._live:
-            self._live = False
-            with torch.cuda.device(self.device):
-                check(load().mk_workspace_release(self.buf.data_ptr()))
+        if not self._live:
+            return
+        if len(self._graphs):
+            raise RuntimeError(f"{len(self._graphs)} HIP graph(s) that captured steps on this workspace are alive: "
+                               "destroy them before releasing it")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("a workspace cannot be released during stream capture")
+        self._live = False
+        with torch.cuda.device(self.device):
+            check(load().mk_workspace_release(self.buf.data_ptr()))
 
     def __del__(self, _finalizing=sys.is_finalizing):
         if getattr(self, "_live", False) and not _finalizing():
-            try:
-                self.release()
-            except Exception:   # never raise from a finaliser
-                pass
+            # no device synchronisation from a finaliser (it may run during a capture):
+            # the next Workspace returns the area
+            self._live = False
+            _deferred.append(_Released(self.device, self.buf))
 
     def read_device_error(self) -> int:
         bits = c_uint32(0)
@@ -226,6 +273,14 @@ def decode_step_noalloc(weights: MkWeights, k_caches: Sequence[torch.Tensor], v_
                    ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, None, 0, current_stream_ptr(), None)
     check(load().mk_decode_step_noalloc(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def noalloc_device_error() -> int:
+    """Sticky device error bits of every faulted ``mk_decode_step_noalloc``
+    step on the current device since the last call (returned and cleared)."""
+    bits = c_uint32(0)
+    check(load().mk_read_device_error(None, c_void_p(current_stream_ptr()), ctypes.byref(bits)))
+    return bits.value
 
 
 def prepare_sampling_params(batch_size: int, top_k, top_p, temperature, device="cuda") -> torch.Tensor:

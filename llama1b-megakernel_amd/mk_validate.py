@@ -4,8 +4,9 @@ The reference validates the megakernel model against the baseline model with
 NxDI's ``logit_validation`` (main.py:347-353), fed with
 
 * ``tol_map = {None: (1e-5, 0.05), 1000: (1e-5, 0.03), 50: (1e-5, 0.03), 5: (1e-5, 0.03)}``
-  (main.py:542): for each top-k of the expected logits (``None`` = all of
-  them) an (atol, rtol) pair;
+  (main.py:544, a string the reference assigns over whatever ``--tol-map``
+  held): for each top-k of the expected logits (``None`` = all of them) an
+  (atol, rtol) pair;
 * ``divergence_difference_tol = 0.001`` (main.py:51): how close the
   expected logits of two tokens must be for a greedy divergence between them
   to count as a tie.
@@ -23,6 +24,7 @@ module restates the checks those numbers parameterise:
 
 from __future__ import annotations
 
+import ast
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -30,6 +32,33 @@ import torch
 REFERENCE_TOL_MAP: Dict[Optional[int], Tuple[float, float]] = {
     None: (1e-5, 0.05), 1000: (1e-5, 0.03), 50: (1e-5, 0.03), 5: (1e-5, 0.03)}
 REFERENCE_DIVERGENCE_TOL = 0.001
+REFERENCE_TOL_MAP_TEXT = "{None: (1e-5, 0.05), 1000: (1e-5, 0.03), 50: (1e-5, 0.03), 5: (1e-5, 0.03)}"
+
+
+def parse_tol_map(text: Optional[str]) -> Dict[Optional[int], Tuple[float, float]]:
+    """``--tol-map`` as the reference writes it (main.py:544): a Python dict
+    literal from top-k (an int, or None for all logits) to (atol, rtol).
+    ``None`` or an empty string gives the reference's map. The literal is read
+    with ``ast.literal_eval`` (no code runs). The reference overwrites the
+    parsed flag with its own map, so on its command line ``--tol-map`` has no
+    effect; this build uses the map it is given."""
+    if text is None or not str(text).strip():
+        return dict(REFERENCE_TOL_MAP)
+    try:
+        m = ast.literal_eval(str(text))
+    except (ValueError, SyntaxError) as e:
+        raise ValueError(f"not a Python literal: {text!r} ({e})") from None
+    if not isinstance(m, dict) or not m:
+        raise ValueError(f"expected a non-empty dict {{top_k: (atol, rtol)}}, got {text!r}")
+    out: Dict[Optional[int], Tuple[float, float]] = {}
+    for k, v in m.items():
+        if not (k is None or (isinstance(k, int) and not isinstance(k, bool) and k >= 1)):
+            raise ValueError(f"top-k key {k!r} is neither None nor a positive int")
+        if not (isinstance(v, (tuple, list)) and len(v) == 2
+                and all(isinstance(x, (int, float)) and not isinstance(x, bool) and x >= 0 for x in v)):
+            raise ValueError(f"value for {k!r} must be (atol, rtol) with non-negative numbers, got {v!r}")
+        out[k] = (float(v[0]), float(v[1]))
+    return out
 
 
 def topk_tolerance(actual: torch.Tensor, expected: torch.Tensor,

@@ -150,6 +150,11 @@ class OracleLlama:
         self.g_final = sd["norm.weight"].to(dt)
         self.scale = SOFTMAX_SCALE_FOR(d.head_dim)
 
+    # The reference casts exp(s - max) to bf16 before the PV product
+    # (attention.py:376-387); a variant with round_p = False keeps p unrounded,
+    # as a split-K kernel must (its per-split maxima differ from the global one).
+    round_p = True
+
     # -- rounding -----------------------------------------------------------
     def rnd(self, x: torch.Tensor) -> torch.Tensor:
         """bf16 rounding point (round-to-nearest-even) in mk mode; identity in exact mode."""
@@ -190,7 +195,7 @@ class OracleLlama:
         p = torch.exp(s - m)
         p = p.masked_fill(mask[None], 0.0)
         den = p.sum(-1, keepdim=True)
-        num = torch.einsum("hts,hsd->htd", self.rnd(p), vv)
+        num = torch.einsum("hts,hsd->htd", self.rnd(p) if self.round_p else p, vv)
         o = num * (1.0 / den)
         return self.rnd(o).permute(1, 0, 2)            # [T, n_q, D]
 

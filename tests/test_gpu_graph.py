@@ -6,7 +6,11 @@ A graph of 12 decode steps (greedy, and with the on-device sampler) is
 captured once and replayed three times, each replay after an eager prefill of
 the prompt on the model's stream: every replay's tokens and final logits equal
 the eagerly launched steps' bit for bit (same kernels, same device state).
+While the graph lives its workspace refuses to be released; once the graph is
+destroyed the release goes through.
 """
+
+import gc
 
 import pytest
 import torch
@@ -45,3 +49,9 @@ def test_graph_replays_match_eager_steps(sampled):
         assert torch.equal(got, eager_tokens)
         assert torch.equal(m.logits[0].cpu(), eager_last)
         assert int(m.pos.item()) == len(ids) - 1 + N
+    # the graph's kernel arguments hold the workspace's exchange area: no release while it lives
+    with pytest.raises(RuntimeError, match="graph"):
+        m.ws.release()
+    del graph
+    gc.collect()
+    m.ws.release()

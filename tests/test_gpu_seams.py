@@ -92,8 +92,72 @@ def test_forward_contract(model):
 
 
 @pytest.mark.timeout(300)
-def test_main_validate_short():
+def test_main_validate_short(tmp_path):
+    """validate with the reference's own flags (main.py:34-105; README.md:48-51)."""
     import main
     rc = main.main(["--mode", "validate", "--enable-nki", "--prompt-len", "24", "--max-new-tokens", "48",
-                    "--seq-len", "128"])
+                    "--seq-len", "128", "--tp-degree", "1", "--torch-dtype", "bfloat16",
+                    "--compiled-model-path", str(tmp_path / "nki"), "--divergence-difference-tol", "0.001",
+                    "--tol-map", "{None: (1e-5, 0.05), 1000: (1e-5, 0.03), 50: (1e-5, 0.03), 5: (1e-5, 0.03)}",
+                    "--num-tokens-to-check", "40", "--on-device-sampling", "--fused-qkv"])
     assert rc == 0
+    assert (tmp_path / "nki" / "mk_compiled.json").exists()
+
+
+@pytest.mark.timeout(300)
+def test_main_generate_reference_flags(tmp_path, capsys):
+    """generate with the reference's flags; --output-logits returns the
+    per-step logits, whose argmax is the generated token."""
+    import main
+    out = main.run_generation(main.parse_args(
+        ["--mode", "generate", "--enable-nki", "--prompt-ids", "5,6,7,8", "--seq-len", "64",
+         "--max-new-tokens", "6", "--compiled-model-path", str(tmp_path / "g"), "--output-logits",
+         "--tp-degree", "1"]))
+    assert out.shape == (1, 6)
+    assert "logits [6, 128256]" in capsys.readouterr().out
+
+
+def test_layer_seam_token_generation(model):
+    """NeuronLlamaDecoderLayerMK (llama_with_megakernel.py:65-204): layer 0
+    runs the 16-layer megakernel, layers 1..15 return the stash with their own
+    (K, V); the result equals the model step's hidden output bit for bit."""
+    from mk_weights import random_token_ids
+    ids = random_token_ids(30, seed=23)
+    model.prefill(ids)                          # pos 29, token ids[29] pending
+    kv0 = model.kv.clone()
+    model.launcher("decode").launch()
+    torch.cuda.synchronize()
+    want_h, want_kv = model.hidden_out.clone(), model.kv.clone()
+    model.kv.copy_(kv0)
+    x = model.packed["embed"][int(ids[29])].reshape(1, 1, -1)
+    pos = torch.tensor([[29]], device="cuda")
+    Y, present = model.layer_stack_forward(x, pos, model.past_key_values)
+    torch.cuda.synchronize()
+    assert torch.equal(Y.reshape(-1), want_h.reshape(-1))
+    assert torch.equal(model.kv, want_kv)
+    for i, (k, v) in enumerate(present):
+        assert k is model.k_caches[i] and v is model.v_caches[i]
+    out0 = model.layers[0](x, position_ids=pos, past_key_value=model.past_key_values[0])
+    cos, sin = out0[2], out0[3]
+    assert cos.shape == sin.shape == (1, 1, 64)
+    assert torch.equal(torch.cat([cos, sin], -1).reshape(-1), model.packed["rope"][29])
+
+
+def test_layer_seam_context_encoding(model):
+    """Context encoding through the layer seam (each layer over the prompt,
+    token by token) writes the same K/V rows as the token-by-token prefill of
+    the 16-layer kernel, bit for bit, and only rows 0..n-1."""
+    from mk_weights import random_token_ids
+    ids = random_token_ids(12, seed=29)
+    model.kv.zero_()
+    model.prefill(torch.cat([ids, ids[:1]]), batched=False)   # rows 0..11 written
+    torch.cuda.synchronize()
+    want = model.kv.clone()
+    model.kv.zero_()
+    x = model.packed["embed"][ids.long().cuda()].reshape(1, 12, -1)
+    pos = torch.arange(12, device="cuda").reshape(1, 12)
+    Y, _ = model.layer_stack_forward(x, pos, None)
+    torch.cuda.synchronize()
+    assert Y.shape == (1, 12, 2048)
+    assert torch.equal(model.kv, want)
+    assert not model.kv[:, :, :, :, 12:].any()

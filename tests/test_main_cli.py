@@ -70,3 +70,128 @@ def test_generate_report_fields():
     assert r["latency_ms_p50"] == 51.0 and r["latency_ms_p90"] == 91.0 and r["latency_ms_p99"] == 100.0
     assert r["latency_ms_p100"] == 100.0 and r["latency_ms_avg"] == 50.5
     assert abs(r["throughput"] - 8 / 0.0505) < 1e-9
+
+
+# ---------------------------------------------------------------------------
+# the reference's flag set (main.py:34-105)
+# ---------------------------------------------------------------------------
+
+README_COMMANDS = [   # README.md:36-51 of the reference, with the flags its megakernel needs
+    "--mode generate --model-path /home/ubuntu/kchern/models/llama-3.2-1b/ --compiled-model-path /tmp/llama1b_baseline",
+    "--mode generate --enable-nki --model-path /home/ubuntu/kchern/models/llama-3.2-1b/ "
+    "--compiled-model-path /tmp/llama1b_nki",
+    "--mode validate --enable-nki --model-path /home/ubuntu/kchern/models/llama-3.2-1b/ "
+    "--compiled-model-path /tmp/llama1b_nki",
+]
+
+
+@pytest.mark.parametrize("cmd", README_COMMANDS)
+def test_reference_readme_commands_parse(cmd):
+    import main
+    for extra in ([], ["--tp-degree", "1", "--seq-len", "1024"]):
+        a = main.parse_args(cmd.split() + extra)
+        assert a.compiled_model_path.startswith("/tmp/llama1b_")
+        assert a.tp_degree == 1 and a.seq_len == 1024 and a.max_length == 1024
+        assert a.torch_dtype == torch.bfloat16
+
+
+def test_every_reference_flag_is_accepted():
+    """One command with every flag of the reference's parser at a value this
+    build can honour."""
+    import main
+    from mk_validate import REFERENCE_TOL_MAP
+    argv = ("--mode validate --llama llama --enable-nki --base-latency 500 --base-throughput 100 "
+            "--model-path random:0 --compiled-model-path /tmp/x --benchmark --divergence-difference-tol 0.002 "
+            "--num-tokens-to-check 8 --prompt hi --top-k 1 --top-p 1.0 --temperature 1.0 "
+            "--global-topk 256 --do-sample True --dynamic --pad-token-id 2 --torch-dtype bfloat16 --batch-size 1 "
+            "--padding-side left --seq-len 1024 --n-active-tokens 1024 --n-positions 131072 "
+            "--max-context-length 1024 --max-new-tokens 16 --max-length 64 --rpl-reduce-dtype float32 "
+            "--output-logits --vocab-parallel --fused-qkv --sequence-parallel-enabled --flash-decoding-enabled "
+            "--on-device-sampling --enable-bucketing True --bucket-n-active-tokens "
+            "--context-encoding-buckets 128 512 1024 --token-generation-buckets 512 1024 --tp-degree 1 "
+            "--qkv-kernel-enabled --attn-kernel-enabled --mlp-kernel-enabled --quantized-kernel-lower-bound 1200 "
+            "--mlp-kernel-fuse-residual-add").split()
+    argv += ["--tol-map", "{None: (1e-5, 0.05), 1000: (1e-5, 0.03), 50: (1e-5, 0.03), 5: (1e-5, 0.03)}"]
+    a = main.parse_args(argv)
+    assert a.tol_map_parsed == REFERENCE_TOL_MAP
+    assert a.divergence_difference_tol == 0.002 and a.num_tokens_to_check == 8
+    assert a.max_length == 1024                   # set from --seq-len as main.py:543 does
+    assert a.context_encoding_buckets == [128, 512, 1024] and a.rpl_reduce_dtype == torch.float32
+
+
+@pytest.mark.parametrize("extra, what", [
+    (["--torch-dtype", "float32"], "--torch-dtype"),
+    (["--tp-degree", "2"], "--tp-degree"),
+    (["--quantized-mlp-kernel-enabled"], "quantized"),
+    (["--rmsnorm-quantize-kernel-enabled"], "quantized"),
+    (["--llama", "my_llama"], "--llama"),
+    (["--n-positions", "512"], "--n-positions"),
+    (["--token-generation-buckets", "4096"], "--token-generation-buckets"),
+    (["--tol-map", "{1000: 0.03}"], "--tol-map"),
+    (["--tol-map", "__import__('os')"], "--tol-map"),
+])
+def test_values_this_build_cannot_honour_are_refused(extra, what):
+    import main
+    with pytest.raises(SystemExit, match=what):
+        main.parse_args(["--mode", "generate"] + extra)
+
+
+@pytest.mark.parametrize("mode", ["evaluate_single", "evaluate_all"])
+def test_contest_modes_exit_out_of_scope(mode):
+    import main
+    with pytest.raises(SystemExit, match="out of scope"):
+        main.parse_args(["--mode", mode, "--enable-nki"])
+
+
+def test_module_selection_and_defaults():
+    import main
+    a = main.parse_args(["--mode", "generate", "--llama", "llama_with_megakernel"])
+    assert a.enable_nki                        # the module name selects the megakernel model
+    a = main.parse_args(["--mode", "generate", "--do-sample", "False"])
+    assert a.do_sample is False
+    # --max-new-tokens defaults to filling --seq-len after the longest prompt (max_length = seq_len)
+    a = main.parse_args(["--mode", "generate", "--seq-len", "1024"])
+    assert main.max_new_tokens(a, [torch.zeros(384), torch.zeros(100)]) == 641
+    a = main.parse_args(["--mode", "generate", "--max-new-tokens", "7"])
+    assert main.max_new_tokens(a, [torch.zeros(384)]) == 7
+
+
+def test_reference_default_prompt_with_a_tokenizer(tok_dir):
+    """No prompt and a tokenizer: the reference's default prompt (main.py:538-539)."""
+    import main
+    args = main.parse_args(["--mode", "generate", "--tokenizer-path", str(tok_dir)])
+    ps = main.encode_prompts(args, main.args_tokenizer(args))
+    assert [p.tolist() for p in ps] == [[8, 9, 3, 4, 5, 6, 7]]
+
+
+def test_tokenizer_saved_into_the_compiled_model_path(tok_dir, tmp_path):
+    import main
+    out = tmp_path / "compiled"
+    args = main.parse_args(["--mode", "generate", "--tokenizer-path", str(tok_dir),
+                            "--compiled-model-path", str(out), "--padding-side", "left"])
+    tok = main.args_tokenizer(args)
+    assert tok.padding_side == "left"
+    assert (out / "tokenizer.json").exists() or (out / "tokenizer_config.json").exists()
+
+
+def test_compiled_model_path_manifest(tmp_path, small):
+    """compile(path) writes the manifest load(path) checks (the reference's
+    --compiled-model-path, main.py:46, 143-150)."""
+    import json
+    from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
+    prod, _ = small
+    cfg = LlamaInferenceConfig(NeuronConfigLlamaMK(seq_len=64, device="cpu"), dims=prod)
+    m = NeuronLlamaForCausalLM("random:0", cfg)
+    with pytest.raises(FileNotFoundError, match="compile"):
+        m.check_manifest(str(tmp_path / "none"))
+    m.compile(str(tmp_path / "c"))
+    m.check_manifest(str(tmp_path / "c"))
+    other = NeuronLlamaForCausalLM("random:1", cfg)
+    with pytest.raises(ValueError, match="model_path"):
+        other.check_manifest(str(tmp_path / "c"))
+    f = tmp_path / "c" / "mk_compiled.json"
+    d = json.loads(f.read_text())
+    d["libmk_sha256"] = "0" * 64
+    f.write_text(json.dumps(d))
+    with pytest.raises(ValueError, match="libmk_sha256"):
+        m.check_manifest(str(tmp_path / "c"))

@@ -11,18 +11,8 @@ set from this floor; the test pins the floor so that choice stays justified.
 
 import torch
 
+from noise_variants import FP64Accumulate as _FP64Accumulate
 from oracle.llama_ref import OracleLlama
-
-
-class _FP64Accumulate(OracleLlama):
-    """The oracle with fp64 accumulation and its bf16 rounding points kept."""
-
-    def __init__(self, sd):
-        super().__init__(sd, mode="exact")
-        self.mode = "mk"
-
-    def rnd(self, x):
-        return x.to(torch.bfloat16).to(self.dt)
 
 
 def test_full_model_step_noise_floor_exceeds_2e2(llama_1b_sd):

@@ -138,6 +138,26 @@ def test_mk_attention_rounding_points():
     assert (got - exact).abs().max() < 1e-2
 
 
+def test_unrounded_p_variant():
+    """round_p = False (the noise-floor variant of a split-K kernel): the
+    numerator uses fp32 p, i.e. the hand-computed case without bf16(p)."""
+    d = Dims(hidden=4, n_q=1, n_kv=1, head_dim=4)
+    o = bare("mk", d)
+    o.round_p = False
+    q = torch.tensor([[[1.0, 0.5, -0.25, 0.125]]])
+    K = torch.tensor([[[0.3, -0.7, 0.2, 0.9], [1.1, 0.4, -0.6, 0.05], [-0.2, 0.8, 0.33, -0.41]]])
+    V = torch.tensor([[[1.0, 2.0, 3.0, 4.0], [-1.5, 0.25, 2.5, -3.0], [0.7, -0.9, 1.3, 0.1]]])
+    V = V.to(torch.bfloat16).float()          # cache rows are bf16
+    s = [0.5 * sum(q[0, 0, e].item() * K[0, j, e].item() for e in range(4)) for j in range(3)]
+    e = [math.exp(x - max(s)) for x in s]
+    expect = [sum(e[j] * V[0, j, c].item() for j in range(3)) / sum(e) for c in range(4)]
+    got = o.attention(q, K, V, torch.tensor([3]))[0, 0]
+    want = torch.tensor(expect, dtype=torch.float32).to(torch.bfloat16).float()
+    assert torch.all((got - want).abs() <= 2 ** -8 * want.abs())
+    o.round_p = True
+    assert not torch.equal(o.attention(q, K, V, torch.tensor([3]))[0, 0], got)
+
+
 def test_oracle_mlp_is_swiglu_of_gate_and_up():
     """The oracle's decoder layer, MLP half (mlp.py:98-192): with the attention's
     output projection zero, layer(h) = h + W_d (silu(W_g n) * (W_u n)), n the
