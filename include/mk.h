@@ -224,6 +224,16 @@ int mk_abi_version(void);
 const char *mk_last_error(void);
 /* Grid size (workgroups, one per CU) the kernel uses on `device`; <0 on error. */
 int mk_grid_size(int device);
+/*
+ * Launch the kernels of `device` on `workgroups` workgroups, one per CU, in
+ * [32, CU count] (0: back to one per CU). Any other count runs the kernels'
+ * generic-grid variants (MI355X's 256 gets variants with the grid size fixed
+ * at compile time), and leaves the other CUs to other work. Applies to the
+ * steps launched after the call; make it with no step of the device in
+ * flight. MK_ERR_SHAPE for a count out of range. No counterpart in the
+ * reference (its NKI kernel runs on one NeuronCore).
+ */
+int mk_set_grid_size(int device, int workgroups);
 /* Frequency of the device wall clock used by the trace (ticks per second). */
 long long mk_wall_clock_hz(int device);
 

@@ -16,19 +16,16 @@ constexpr int BATT_MAX_SPLIT = 16;  // KV-length splits per (sequence, kv head)
 // Workspace of a batched step (max batch M >= 2), bytes:
 //   [0, 256)          control words (exit counter, error bits, epoch), as for batch 1
 //   256 + 256*b       u64 argmax key of sequence b (one 256-byte line each)
-//   BWS_CNT0(M) + set*bws_cnt_set(M)     arrival counters of one launch (two sets,
-//                     alternating by epoch; each launch zeroes the other set):
+// Arrival counters of one launch, set*bws_cnt_set(M) into the exchange area's
+// uncached counter block (two sets, alternating by epoch; each launch zeroes
+// the other set):
 //     hand-over counters [MK_MAX_LAYERS][5 hand-overs][N_SUB sub-counters], one 128-byte line each
 //     attention-split counters u32 [MK_MAX_LAYERS][M][8 kv heads]
 //     down-projection row-group counters u32 [MK_MAX_LAYERS][DN_MAX]
 constexpr size_t BWS_KEY0 = 256;
 constexpr size_t BWS_KEY_STRIDE = 256;
 constexpr int N_HANDOVER = 5;   // per layer: qkv, att, h1, act, h2
-#ifndef MK_NSUB
-#define MK_NSUB 32   // (8 lines: ~1% slower at batch 8, arrivals to one line serialise)
-#endif
-constexpr int N_SUB = MK_NSUB;  // sub-counters per hand-over (arrivals spread over N_SUB lines)
-static_assert(N_SUB % 8 == 0 && N_SUB <= 64, "8, 16, .. 64 sub-counters");
+constexpr int N_SUB = 32;       // sub-counters per hand-over (arrivals spread over N_SUB lines)
 constexpr size_t CNT_LINE = 128;
 constexpr size_t HCNT_BYTES = (size_t)MK_MAX_LAYERS * N_HANDOVER * N_SUB * CNT_LINE;
 constexpr int DN_MAX = 256;     // row groups of the 2-D down projection (grid / 4) at most
@@ -37,14 +34,10 @@ __host__ __device__ inline size_t bws_cnt0(int M) { return BWS_KEY0 + (size_t)M 
 __host__ __device__ inline size_t bws_cnt_set(int M) {
   return HCNT_BYTES + (size_t)MK_MAX_LAYERS * M * MK_N_KV_HEADS * 4 + (size_t)MK_MAX_LAYERS * DN_MAX * 4;
 }
-__host__ __device__ inline size_t batch_ws_bytes(int M) { return bws_cnt0(M) + 2 * bws_cnt_set(M); }
-// The two counter sets of a batched launch live in a block of uncached device
-// memory owned by the workspace's exchange area (sized for BATCH_MAX, so any
-// block serves any batch), unless built with MK_BCNT_UNCACHED=0, which keeps
-// them in the workspace at bws_cnt0(M).
-#ifndef MK_BCNT_UNCACHED
-#define MK_BCNT_UNCACHED 1
-#endif
+__host__ __device__ inline size_t batch_ws_bytes(int M) { return bws_cnt0(M); }
+// The two counter sets of a batched launch (2 * bws_cnt_set(M) bytes) live in
+// a block of uncached device memory owned by the workspace's exchange area
+// (sized for BATCH_MAX, so any block serves any batch).
 constexpr size_t BCNT_BLOCK_BYTES = 2 * ((size_t)HCNT_BYTES + (size_t)MK_MAX_LAYERS * BATCH_MAX * MK_N_KV_HEADS * 4 +
                                          (size_t)MK_MAX_LAYERS * DN_MAX * 4);
 // Largest batch a workspace of `bytes` serves with the batched layout (< 2: batch-1 layout).

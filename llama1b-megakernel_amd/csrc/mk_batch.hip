@@ -48,63 +48,14 @@
 #include "mk_batch.h"
 #include "mk_common.h"
 
-#ifndef MK_BATT_DEPTH
-#define MK_BATT_DEPTH 1
-#endif
-#ifndef MK_BATT_MX
-#define MK_BATT_MX 1       // attention scores on the matrix cores (attn_item_mx)
-#endif
-#ifndef MK_BGU_PRE
-#define MK_BGU_PRE 1
-#endif
-#ifndef MK_BDOWN_2D
-#define MK_BDOWN_2D 1
-#endif
-#ifndef MK_BDOWN_2D_MT1
-#define MK_BDOWN_2D_MT1 0  // the 2-D down projection at batches of up to 16 too
-#endif
-#ifndef MK_BGFIX_256
-#define MK_BGFIX_256 1     // the grid-size-256 instantiations on 256-CU devices
-#endif
-#ifndef MK_BLM_ODD
-#define MK_BLM_ODD 100     // lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
-#endif
-#ifndef MK_BLM_COLLECT
-#define MK_BLM_COLLECT 1   // one token tile: a workgroup's logits collected in LDS, stored after its last round
-#endif
-#ifndef MK_BQKV_WNORM
-#define MK_BQKV_WNORM 1    // QKV: each wave normalises the K quarter it multiplies, in registers
-#endif
-#ifndef MK_BATT_ROUNDS
-#define MK_BATT_ROUNDS 1   // attention ranges per workgroup
-#endif
-#ifndef MK_BGU_LDS
-#define MK_BGU_LDS 1       // one tile: the last gate/up weight unit copied to LDS during the waits before it
-#endif
-#ifndef MK_BGU_CH
-#define MK_BGU_CH 4        // its 1 KiB copies per wave issued per poll round of that wait
-#endif
-#ifndef MK_BGU_CH_O
-#define MK_BGU_CH_O 8      // its copies per wave per poll round of the attention-output wait (O phase)
-#endif
-#ifndef MK_BGU_SKIP_O
-#define MK_BGU_SKIP_O 1    // failed polls of that wait before its copies start
-#endif
-#ifndef MK_BGU_HALF
-#define MK_BGU_HALF 1      // at most 8 tokens: half of gate/up unit 2 copied to the staged matrix's padding rows
-#endif
-#ifndef MK_BO_PAIR
-#define MK_BO_PAIR 1       // 8-row O shares at batches up to 8: each operand load carries two k-steps
-#endif
-#ifndef MK_BDN_PAIR
-#define MK_BDN_PAIR 1      // 8-row down shares: each operand load carries two k-steps
-#endif
-#ifndef MK_BDN_RING
-#define MK_BDN_RING 4      // its weight/act units in flight per wave
-#endif
-#ifndef MK_BDN_PRE
-#define MK_BDN_PRE 4       // of which issued before the act wait (weights only)
-#endif
+// Tuning constants (values measured best on MI355X; the alternatives and their
+// results are recorded with the design notes).
+constexpr int BATT_DEPTH = 1;   // 128-row K/V groups an attention item keeps in flight ahead
+constexpr int BGU_CH = 4;       // one tile: 1 KiB gate/up LDS copies per wave per poll round of the h1 wait
+constexpr int BGU_CH_O = 8;     // ... of the attention-output wait (O phase)
+constexpr int BGU_SKIP_O = 1;   // failed polls of that wait before its copies start
+constexpr int BDN_RING = 4;     // down projection: weight/act units in flight per wave
+constexpr int BDN_PRE = 4;      // of which issued before the act wait (weights only)
 
 namespace {
 
@@ -178,7 +129,7 @@ struct BLds {
   // gw[(w*KS + s)*64], lane l's 16 bytes at + l, the register unit's lane
   // order), and a 1 KiB area per wave that copies past it write (two tiles
   // leave no room in LDS for either)
-  static constexpr int GW = MT == 1 && MK_BGU_LDS ? NWAVE * KS * 64 : 1;
+  static constexpr int GW = MT == 1 ? NWAVE * KS * 64 : 1;
   u32x4 gw[GW];
   u32x4 gspare[GW > 1 ? NWAVE * 64 : 1];
 };
@@ -732,8 +683,7 @@ __device__ __forceinline__ void plan_and_rope(BCtx& c, BLds<MT>& L) {
     // groups, as equal as possible; a piece is one item. Every item beyond the
     // first on a workgroup costs a few us of fixed work (q hand-over, partial
     // publication, merge), so the plan is the smallest piece size m (in
-    // groups, found by bisection) whose items fit MK_BATT_ROUNDS rounds of the
-    // grid: p_b = ceil(groups_b / m), at most 16 splits per segment. Items are
+    // groups, found by bisection) whose items fit one round of the grid: p_b = ceil(groups_b / m), at most 16 splits per segment. Items are
     // listed (sequence, kv head, piece). Lane b of wave 0 plans sequence b, in
     // 32-bit arithmetic (s_max <= 2^20 and batch <= 32 keep every count below
     // 2^25).
@@ -742,7 +692,7 @@ __device__ __forceinline__ void plan_and_rope(BCtx& c, BLds<MT>& L) {
     const uint32_t n = on ? (uint32_t)L.pos[lane] + 1u : 0u;
     const uint32_t ng = (n + ATT_GROUP - 1u) / ATT_GROUP;      // 128-row groups per kv head
     const uint32_t max_ng = wave_max_u32(ng);
-    const uint32_t slots = (uint32_t)MK_BATT_ROUNDS * (uint32_t)c.G;
+    const uint32_t slots = (uint32_t)c.G;
     auto pieces = [&](uint32_t m) { return on ? (ng + m - 1u) / m : 0u; };
     uint32_t lo = (max_ng + BATT_MAX_SPLIT - 1u) / BATT_MAX_SPLIT, hi = max_ng;   // <= 16 splits per segment
     if (lo < 1u) lo = 1u;
@@ -798,29 +748,24 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L, u32x4 (&
   trace_mark(c.s, 2 * xk(li, 1) - 1);
   if (!FIRST) {
     wait_h2(c, li - 1);
-    if (MK_BQKV_WNORM) {
-      stage_issue<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, L);
-      stage_wait_raw<MT, 0>(c, R0, R1, L);
-    } else {
-      stage_norm<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, nullptr, R0, R1, L);
-    }
+    stage_issue<MT>(c, make_rsrc(c.xb(li - 1, p.lay.h2), (size_t)c.B * H * 2), false, L);
+    stage_wait_raw<MT, 0>(c, R0, R1, L);
   } else {   // the first layer: its input is final data; the plan runs while it lands
     if (p.hidden_in) stage_issue<MT>(c, make_rsrc(p.hidden_in, (size_t)c.B * H * 2), false, L);
     else stage_issue<MT>(c, make_rsrc(p.embed, EMBED_BYTES), true, L);
     if (MT == 1) plan_and_rope<MT>(c, L);   // (two tiles: in the prologue; inlined here it spills)
-    if (MK_BQKV_WNORM) stage_wait_raw<MT, 0>(c, R0, R1, L);
-    else stage_finish<MT, 0>(c, nullptr, R0, R1, L);
+    stage_wait_raw<MT, 0>(c, R0, R1, L);
   }
-  u32x4 an[MK_BQKV_WNORM ? MT * KS : 1];
-  if constexpr (MK_BQKV_WNORM) qkv_norm_a<MT>(L, an);
+  // each wave normalises the K quarter it multiplies, in its A-operand registers
+  u32x4 an[MT * KS];
+  qkv_norm_a<MT>(L, an);
   trace_mark(c.s, 2 * xk(li, 1));
   uint16_t* xq = c.sx(li, p.lay.sq_qkv);
   for (int tt = 0; tt < ntile; ++tt) {
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (MK_BQKV_WNORM) mma_reg<MT, KS>(an, wv, acc);
-    else mma_lds<MT>(L, wave * KQ, wv, acc);
+    mma_reg<MT, KS>(an, wv, acc);
     if (tt + 1 < ntile) load_w<KS>(rw, p.tiled, row0 + 16 * (tt + 1), row_end, H * 2, wave * KQ, wv);
     // every wave finishes a share of the outputs: token tile wave % MT, and
     // IPW of the 4 output rows of each lane (rows (lane/16)*4 + i of the tile)
@@ -899,21 +844,16 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       const int ps = L.pos[b];
       const int j0 = ga * ATT_GROUP, j1 = min(gb * ATT_GROUP, ps + 1);
       const bool fresh = ps >= j0 && ps < j1;
-      // the item's cached rows do not depend on this step: its first MK_BATT_DEPTH groups are issued
+      // the item's cached rows do not depend on this step: its first BATT_DEPTH groups are issued
       // before the wait for q (in a prefill step rows of this step's tokens are among them: issued after it)
       const size_t head = (size_t)(c.cache_seq(b) * NKV + h) * p.s_max * HD;
       AttnRows ar;
       ar.init(p.kc[li] + head, p.vc[li] + head, p.s_max, j0, min(j1, ps));
-#if MK_BATT_MX
-      AttnGroupMx ring[MK_BATT_DEPTH + 1];
+      AttnGroupMx ring[BATT_DEPTH + 1];
       auto issue_ahead = [&]() {
 #pragma unroll
-        for (int g = 0; g < MK_BATT_DEPTH; ++g) load_mx(ar, g, ring[g]);
+        for (int g = 0; g < BATT_DEPTH; ++g) load_mx(ar, g, ring[g]);
       };
-#else
-      AttnGroup g0;   // (attn_item issues its second group itself at depth 2)
-      auto issue_ahead = [&]() { ar.load(0, g0); };
-#endif
       if (!c.prefill) issue_ahead();
       if (wave_id() == 0) {
         if (!waited) trace_mark(c.s, 2 * xk(li, 2) - 1);
@@ -933,19 +873,15 @@ __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
       waited = true;
       lds_sync();
       if (c.prefill) issue_ahead();
-#if MK_BATT_MX
       // the head's only split writes the final output, no partial (with two
       // MFMA tiles, where every head has one split at long contexts)
       const bool only = MT == 2 && nsb == 1;
-      attn_item_mx<MK_BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att,
-                                  only ? c.xb(li, p.lay.att) : nullptr, b, h * GQA * HD);
+      attn_item_mx<BATT_DEPTH>(ar, ring, L.q, fresh, c.part(li, b, h, sp), L.att,
+                               only ? c.xb(li, p.lay.att) : nullptr, b, h * GQA * HD);
       if (only) {
         arrive(c.ho(li, HO_ATT), (b * NKV + h) % N_SUB);
         continue;
       }
-#else
-      attn_item<MK_BATT_DEPTH>(ar, g0, L.q, fresh, c.part(li, b, h, sp), L.att);
-#endif
       // publish the partial and count it in; the last arrival merges
       wait_mem();
       lds_sync();
@@ -979,7 +915,7 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, GuCopy& gu
   const int ntile = (R1 - R0 + 15) / 16;
   const rsrc_t rw = make_rsrc(p.w_o + (size_t)l * H * H, O_LAYER_BYTES);
   // at most 8 rows and 8 tokens: paired operand loads (pair_w_off), half the loads
-  const bool pr = MT == 1 && MK_BO_PAIR && c.dpair && c.B <= 8;
+  const bool pr = MT == 1 && c.dpair && c.B <= 8;
   const uint32_t wo = pair_w_off(p.tiled, R0, R1, H * 2), wstep = pair_wstep(p.tiled);
   const int ks0 = wave * (KQ / 32);
   u32x4 wv[KS];
@@ -991,9 +927,9 @@ __device__ __forceinline__ void phase_o(BCtx& c, int li, BLds<MT>& L, GuCopy& gu
   }
   trace_mark(c.s, 2 * xk(li, 3) - 1);
   // every (sequence, kv head) merge adds to sub-counter (b*8 + h) % N_SUB
-  if constexpr (BLds<MT>::GW > 1 && MK_BGU_CH_O > 0)
-    wait_handover_copy(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB, guc, MK_BGU_CH_O,
-                       &L.gw[wave * KS * 64], MK_BGU_SKIP_O);
+  if constexpr (BLds<MT>::GW > 1)
+    wait_handover_copy(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB, guc, BGU_CH_O,
+                       &L.gw[wave * KS * 64], BGU_SKIP_O);
   else
     wait_handover(c.s, c.ho(li, HO_ATT), c.B * NKV / N_SUB, c.B * NKV % N_SUB);
   trace_mark(c.s, 2 * xk(li, 3));
@@ -1050,7 +986,7 @@ __device__ __forceinline__ void gu_copy_init(const BCtx& c, int li, BLds<MT>& L,
   const rsrc_t rw = make_rsrc(p.w_gu + (size_t)(p.first_layer + li) * 2 * INTER * H, GU_LAYER_BYTES);
   constexpr bool GL = BLds<MT>::GW > 1;
   gc.u3.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, (H / (KS * 32) - 1) * KS * 32, GL && my_tiles == 1);
-  gc.half = GL && MK_BGU_HALF && c.B <= 8 && ntile == NWAVE;
+  gc.half = GL && c.B <= 8 && ntile == NWAVE;
   gc.u2.init(rw, p.tiled, row0 + 16 * wave, row_end, H * 2, 2 * KS * 32, gc.half);
   gc.d3 = &L.gw[GL ? wave * KS * 64 : 0];
   gc.d2 = reinterpret_cast<u32x4*>(&L.xn[MT == 1 ? 8 : 0][0]) + wave * (KS / 2) * 64;
@@ -1085,23 +1021,21 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, GuCopy& g
   u32x4* spare = &L.gspare[GL ? wave * 64 : 0];
   // with at most 8 tokens, the first half of unit 2 is in LDS too (gc.u2)
   const bool half = gl && gc.half;
-  // MK_BGU_PRE weight units are issued before the h1 wait, the others right
-  // behind the h1 staging copies, so the staging does not queue behind them
-  if (MK_BGU_PRE >= 1) issue(0, wa);
-  if (MK_BGU_PRE >= 2) issue(1, wb);
+  // one weight unit is issued before the h1 wait, the other right behind the
+  // h1 staging copies, so the staging does not queue behind it
+  issue(0, wa);
   trace_mark(c.s, 2 * xk(li, 4) - 1);
-  if (GL) wait_handover_copy(c.s, c.ho(li, HO_H1), c.G / N_SUB, c.G % N_SUB, gc, MK_BGU_CH, gdst);
+  if (GL) wait_handover_copy(c.s, c.ho(li, HO_H1), c.G / N_SUB, c.G % N_SUB, gc, BGU_CH, gdst);
   else wait_grid(c, li, HO_H1);
   stage_issue<MT>(c, make_rsrc(c.xb(li, p.lay.h1), (size_t)c.B * H * 2), false, L, gc.half ? spare : nullptr);
-  if (MK_BGU_PRE < 1) issue(0, wa);
-  if (MK_BGU_PRE < 2) issue(1, wb);
+  issue(1, wb);
   if (GL) {
     gc.u3.issue_fixed<KS>(gdst, spare);
     gc.u2.issue_fixed<KS / 2>(gc.d2, spare);
   }
   // the raw columns kept for the down projection's residual: its rows
   const int D0 = c.d2 ? (c.w / DN_KQ) * c.drpg : R0, D1 = c.d2 ? D0 + c.drpg : R1;
-  stage_finish<MT, (2 - MK_BGU_PRE) * KS + (GL ? KS + KS / 2 : 0)>(c, nullptr, D0, D1, L);
+  stage_finish<MT, KS + (GL ? KS + KS / 2 : 0)>(c, nullptr, D0, D1, L);
   trace_mark(c.s, 2 * xk(li, 4));
   uint16_t* act = c.xb(li, p.lay.act);
   f32x4 acc[MT];
@@ -1234,8 +1168,8 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   constexpr int KW = INTER / NWAVE;       // 2048 columns per wave
   constexpr int UPT = KW / (DKS * 32);    // 8 units (one tile)
   constexpr int NP = DKS / 2;             // k-step pairs per unit
-  constexpr int NR = MK_BDN_RING;
-  static_assert(UPT % NR == 0 && MK_BDN_PRE <= NR, "down ring");
+  constexpr int NR = BDN_RING;
+  static_assert(UPT % NR == 0 && BDN_PRE <= NR, "down ring");
   const rsrc_t rw = make_rsrc(p.w_d + (size_t)l * H * INTER, D_LAYER_BYTES);
   const rsrc_t ra = make_rsrc(c.xb(li, p.lay.act), (size_t)((c.B + 15) / 16 * 16) * INTER * 2);
   const uint32_t wo = pair_w_off(p.tiled, R0, R1, INTER * 2), wstep = pair_wstep(p.tiled);
@@ -1257,13 +1191,13 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   };
   Unit ring[NR];
 #pragma unroll
-  for (int s = 0; s < MK_BDN_PRE; ++s) issue_w(s, ring[s]);
+  for (int s = 0; s < BDN_PRE; ++s) issue_w(s, ring[s]);
   trace_mark(c.s, 2 * xk(li, 5) - 1);
   wait_grid(c, li, HO_ACT);
   trace_mark(c.s, 2 * xk(li, 5));
 #pragma unroll
   for (int s = 0; s < NR; ++s) {
-    if (s >= MK_BDN_PRE) issue_w(s, ring[s]);
+    if (s >= BDN_PRE) issue_w(s, ring[s]);
     issue_a(s, ring[s]);
   }
   f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -1451,10 +1385,8 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   int V0, V1, R0, R1;
   // vocabulary rows in multiples of 8: in the tiled lm_head the 8 rows of a
   // lane group are one 128-byte run of each block (a share of 501 rows would
-  // split most 16-row tiles between two workgroups at odd offsets). Workgroup
-  // w runs on XCD w % 8; MK_BLM_ODD < 100 gives the odd-numbered ones (the odd
-  // XCDs) fewer rows.
-  share_parity(VOCAB / 8, c.G, c.w, 100, MK_BLM_ODD, V0, V1);
+  // split most 16-row tiles between two workgroups at odd offsets).
+  share(VOCAB / 8, c.G, c.w, V0, V1);
   V0 *= 8;
   V1 *= 8;
   share(H, c.G, c.w, R0, R1);
@@ -1479,7 +1411,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
   // the whole share instead: each wave writes its tiles there, with no
   // workgroup barrier per round, and the share leaves after the last round as
   // one contiguous run per token
-  constexpr bool LGC = BLds<MT>::GW > 1 && MK_BLM_COLLECT;
+  constexpr bool LGC = BLds<MT>::GW > 1;
   constexpr int LG_ROWS = 512, LG_STRIDE = LG_ROWS + 4;   // +4 floats: the lane groups' tokens on distinct banks
   static_assert(!LGC || sizeof(L.gw) >= sizeof(float) * 16 * MT * LG_STRIDE, "logit collection area");
   const bool lgc = LGC && V1 - V0 <= LG_ROWS;
@@ -1618,7 +1550,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.drpg = c.dng > 0 ? H / c.dng : 0;
   // (batch 8 measured slower with it: there act is small and the extra hand-over costs more)
   c.dpair = (H + c.G - 1) / c.G <= 8;
-  c.d2 = MK_BDOWN_2D && (MT == 2 || MK_BDOWN_2D_MT1) && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
+  c.d2 = MT == 2 && c.G % DN_KQ == 0 && c.dng <= DN_MAX && c.dng * c.drpg == H && c.drpg % 16 == 0 &&
          c.drpg <= RES_MAX;
   c.sset = p.xch + p.lay.sent_base + (size_t)(epoch & 1u) * p.lay.sset;
   c.cnt_other = reinterpret_cast<uint32_t*>(cnt0 + (size_t)((epoch + 1u) & 1u) * cset);
@@ -1657,7 +1589,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
       phase_gu<MT>(c, li, L, guc);
       if (c.d2) {
         phase_down2d<MT>(c, li, L);
-      } else if constexpr (MT == 1 && MK_BDN_PAIR) {
+      } else if constexpr (MT == 1) {
         if (c.dpair && c.B <= 8) phase_down_pair<MT>(c, li, L);
         else phase_down<MT>(c, li, L);
       } else {
@@ -1714,7 +1646,7 @@ namespace mk {
 // 16-row MFMA tile up to 16 tokens, two above; MI355X's 256 CUs get the
 // instantiations with the grid size fixed at compile time.
 const void* batch_kernel_for(int batch, int grid) {
-  if (grid == 256 && MK_BGFIX_256)
+  if (grid == 256)
     return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 256>)
                        : reinterpret_cast<const void*>(mk_batch_kernel<2, 256>);
   return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 0>)

@@ -340,20 +340,6 @@ __device__ __forceinline__ void share(int total, int n, int i, int& lo, int& hi)
   }
 }
 
-// Share [lo, hi) of `total` items for part i of n, even-numbered parts
-// weighing `a` and odd-numbered ones `b` (a, b in 1..100).
-__device__ __forceinline__ void share_parity(int total, int n, int i, int a, int b, int& lo, int& hi) {
-  auto wsum = [&](int k) { return (uint32_t)(((k + 1) >> 1) * a + (k >> 1) * b); };
-  const uint32_t s = wsum(n);
-  if ((unsigned long long)(unsigned)total * s <= 0xffffffffull) {
-    lo = (int)((uint32_t)total * wsum(i) / s);
-    hi = (int)((uint32_t)total * wsum(i + 1) / s);
-  } else {
-    lo = (int)((unsigned long long)total * wsum(i) / s);
-    hi = (int)((unsigned long long)total * wsum(i + 1) / s);
-  }
-}
-
 // Sentinel tests. bf16 exchange data: any 16-bit lane equal to 0xffff.
 // fp32 exchange data: a whole word equal to 0xffffffff.
 __device__ __forceinline__ bool sent_bf16(uint32_t w) { return (w | 0xffff0000u) == 0xffffffffu || w >= 0xffff0000u; }
@@ -547,7 +533,6 @@ struct AttnGroupT {
   u32x4 k[R], v[R];
   bool valid[R];
 };
-using AttnGroup = AttnGroupT<>;
 struct AttnRows {
   rsrc_t rk, rv;
   int j0, jc;
@@ -582,10 +567,10 @@ struct AttnRows {
 // (the cached rows do not depend on the current step, so a caller issues them
 // before it waits for q). q_lds: bf16 q[4][64] | fresh k[64] | fresh v[64] in LDS.
 // Thread t serves row (t >> 3) of each 32-row round and the 8 dims (t & 7)*8..
-// of it; rows stream in groups of ATT_GROUP with an online softmax, DEPTH
-// (1 or 2) groups ahead in flight. Writes the item's partial (m[4], l[4],
-// o[4][64]) unnormalised, relative to m.
-template <int DEPTH = 1, int R = ATT_R>
+// of it; rows stream in groups of ATT_GROUP with an online softmax, the next
+// group in flight. Writes the item's partial (m[4], l[4], o[4][64])
+// unnormalised, relative to m.
+template <int R = ATT_R>
 __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& first, const uint16_t* q_lds,
                                           bool fresh, float* part, AttnShared& sh) {
   const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
@@ -639,7 +624,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& f
       m_run[g] = mn;
     }
   };
-  // cached rows in groups of R rounds, the loads of the next DEPTH groups in flight while one is
+  // cached rows in groups of R rounds, the loads of the next group in flight while one is
   // consumed. The buffers rotate by unrolling (a register copy of a buffer whose loads are in
   // flight would wait for them), and the loads ahead are issued unconditionally (rows past the
   // item read nothing: out-of-range offsets), so the compiler's wait before each consume counts
@@ -686,7 +671,7 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& f
     }
   };
   auto step = [&](int gi, AttnGroupT<R>& cur, AttnGroupT<R>& ahead) {
-    rows.load(gi + DEPTH, ahead);   // past the last group: all rows invalid, nothing read
+    rows.load(gi + 1, ahead);   // past the last group: all rows invalid, nothing read
     if (gi < ngroups) {
       const int left = rows.jc - rows.j0 - gi * 32 * R;   // rows of this group and beyond
       if (left >= 32 * R) consume_full(cur, BoolC<false>());
@@ -694,20 +679,10 @@ __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& f
     }
   };
   AttnGroupT<R>& A = first;
-  if (DEPTH == 1) {
-    AttnGroupT<R> B;
-    for (int gi = 0; gi < ngroups; gi += 2) {
-      step(gi, A, B);
-      step(gi + 1, B, A);
-    }
-  } else {
-    AttnGroupT<R> B, C;
-    rows.load(1, B);
-    for (int gi = 0; gi < ngroups; gi += 3) {
-      step(gi, A, C);
-      step(gi + 1, B, A);
-      step(gi + 2, C, B);
-    }
+  AttnGroupT<R> B;
+  for (int gi = 0; gi < ngroups; gi += 2) {
+    step(gi, A, B);
+    step(gi + 1, B, A);
   }
   if (fresh) {   // the new row: row-lane 0 of one round
     const bool valid[1] = {rl == 0};

@@ -73,57 +73,26 @@ namespace {
 
 using namespace mk;
 
-// KV-length splits per kv head (attention work items) and rounds of 32 rows
-// per attention group
-#ifndef MK_ATT_SPLITS
-#define MK_ATT_SPLITS 8
-#endif
-#ifndef MK_GFIX_256
-#define MK_GFIX_256 1      // the grid-size-256 instantiation on 256-CU devices
-#endif
-#ifndef MK_ATT_ROUNDS
-#define MK_ATT_ROUNDS 4
-#endif
-constexpr int ATT_MAX_SPLIT = MK_ATT_SPLITS;
-constexpr int ATT_RD = MK_ATT_ROUNDS;
+// Tuning constants (values measured best on MI355X; the alternatives and their
+// results are recorded with the design notes).
+constexpr int ATT_MAX_SPLIT = 8;           // KV-length splits per kv head (attention work items)
+constexpr int ATT_RD = 4;                  // rounds of 32 rows per attention group
 constexpr int GU_LDS_PAIRS = 4;            // gate/up pairs per wave copied HBM -> LDS ahead of the GU phase
 // 1 KiB chunks of that copy issued per poll round of the layer-input wait and
 // of the attention-output wait
-#ifndef MK_GU_STEP_QKV
-#define MK_GU_STEP_QKV 8
-#endif
-#ifndef MK_GU_STEP_O
-#define MK_GU_STEP_O 6
-#endif
-constexpr int GU_LDS_STEP_QKV = MK_GU_STEP_QKV, GU_LDS_STEP_O = MK_GU_STEP_O;
+constexpr int GU_LDS_STEP_QKV = 8, GU_LDS_STEP_O = 6;
 constexpr int O_RING = 4;                  // O rows per wave in the register ring
 // Gate/up pairs per wave (after the LDS ones) loaded into registers before the
 // attention-output wait on workgroups with O rows, so that the h1 wait queues
 // behind fewer weight loads; the other GU_RING pairs of the wave's first eight
 // are issued after the O projection.
-#ifndef MK_GU_EARLY
-#define MK_GU_EARLY 2
-#endif
-constexpr int GU_EARLY = MK_GU_EARLY;
+constexpr int GU_EARLY = 2;
 constexpr int GU_RING = 4 - GU_EARLY;
-static_assert(GU_EARLY >= 0 && GU_RING >= 1, "gate/up register split");
 // 1 KiB chunks of the wave's first down-projection row loaded before the
 // gate/up dot products (they land while those run, so the act store that
 // queues behind them is not delayed, and HBM is not idle meanwhile).
-#ifndef MK_D_EARLY
-#define MK_D_EARLY 8
-#endif
-constexpr int D_EARLY = MK_D_EARLY;
-static_assert(D_EARLY >= 0 && D_EARLY <= 16, "down-projection early chunks");
-// lm_head rows per wave in the register ring (4 KiB each)
-#ifndef MK_LM_RING
-#define MK_LM_RING 8
-#endif
-// lm_head rows of an odd-numbered workgroup per 100 of an even-numbered one
-#ifndef MK_LM_ODD
-#define MK_LM_ODD 100
-#endif
-static_assert(MK_LM_ODD > 0 && MK_LM_ODD <= 100, "lm_head parity weight");
+constexpr int D_EARLY = 8;
+constexpr int LM_RING = 8;                 // lm_head rows per wave in the register ring (4 KiB each)
 constexpr int MIN_GRID = 32;
 constexpr int MAX_GRID = 1024;
 
@@ -770,8 +739,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     // ---- final norm + tied lm_head + argmax ----
     if (p.do_lm) {
       int V0, V1;
-      share_parity(VOCAB, G, w, 100, MK_LM_ODD, V0, V1);
-      RowStream<MK_LM_RING, 4> ls;
+      share(VOCAB, G, w, V0, V1);
+      RowStream<LM_RING, 4> ls;
       const Span sp = wave_span(V0, V1);
       ls.start(make_rsrc(p.embed, EMBED_BYTES), (uint32_t)sp.lo * (H * 2), H * 2, sp.n);
       trace_mark(c.s, 2 * xk(p.n_layers, 1) - 1);
@@ -878,7 +847,8 @@ int fail(int code, const char* fmt, ...) {
 
 struct DeviceInfo {
   int ready;
-  int grid;
+  int grid;        // workgroups per launch: the CU count, or the mk_set_grid_size override
+  int cus;
   unsigned long long ticks_per_s;
   int status;
 };
@@ -888,7 +858,7 @@ std::mutex g_dev_mu;
 // The batch-1 kernel for a grid of `grid` workgroups (one per CU): MI355X's 256
 // CUs get the instantiation with the grid size fixed at compile time.
 const void* decode_kernel_for(int grid) {
-  return grid == 256 && MK_GFIX_256 ? reinterpret_cast<const void*>(mk_decode_kernel<256>)
+  return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256>)
                      : reinterpret_cast<const void*>(mk_decode_kernel<0>);
 }
 
@@ -903,6 +873,7 @@ int device_info(int dev, DeviceInfo* out) {
         hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
       return fail(MK_ERR_HIP, "hipDeviceGetAttribute failed on device %d", dev);
     d.grid = cus;
+    d.cus = cus;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel_for(cus), NT, 0) != hipSuccess)
       return fail(MK_ERR_HIP, "occupancy query failed");
     d.ticks_per_s = (unsigned long long)(clk_khz > 0 ? clk_khz : 100000) * 1000ull;
@@ -1191,6 +1162,18 @@ int mk_grid_size(int device) {
   return rc == MK_OK ? d.grid : rc;
 }
 
+int mk_set_grid_size(int device, int workgroups) {
+  DeviceInfo d;
+  const int rc = device_info(device, &d);
+  if (rc != MK_OK) return rc;
+  if (workgroups != 0 && (workgroups < MIN_GRID || workgroups > d.cus))
+    return fail(MK_ERR_SHAPE, "grid of %d workgroups not in [%d, %d] (the CU count) on device %d", workgroups,
+                MIN_GRID, d.cus, device);
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  g_dev[device].grid = workgroups ? workgroups : g_dev[device].cus;
+  return MK_OK;
+}
+
 long long mk_wall_clock_hz(int device) {
   DeviceInfo d;
   const int rc = device_info(device, &d);
@@ -1305,8 +1288,7 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
                   batch_ws_bytes(xe.max_batch));
     const int brc = batch_device_check(dev, g_msg, sizeof(g_msg));
     if (brc != MK_OK) return brc;
-    uint8_t* cnt = MK_BCNT_UNCACHED ? xe.cnt : static_cast<uint8_t*>(a->workspace) + bws_cnt0(xe.max_batch);
-    const hipError_t be = batch_launch(w, a, xe.xch, cnt, xe.max_batch, di.grid, di.ticks_per_s * 2ull);
+    const hipError_t be = batch_launch(w, a, xe.xch, xe.cnt, xe.max_batch, di.grid, di.ticks_per_s * 2ull);
     if (be != hipSuccess) return fail(MK_ERR_HIP, "batched kernel launch failed: %s", hipGetErrorString(be));
     return MK_OK;
   }

@@ -91,6 +91,8 @@ def load() -> ctypes.CDLL:
         lib.mk_last_error.restype = c_char_p
         lib.mk_grid_size.argtypes = [c_int]
         lib.mk_grid_size.restype = c_int
+        lib.mk_set_grid_size.argtypes = [c_int, c_int]
+        lib.mk_set_grid_size.restype = c_int
         lib.mk_wall_clock_hz.argtypes = [c_int]
         lib.mk_wall_clock_hz.restype = ctypes.c_longlong
         lib.mk_workspace_bytes.argtypes = [c_int32, c_int32]
@@ -273,6 +275,21 @@ def decode_step_noalloc(weights: MkWeights, k_caches: Sequence[torch.Tensor], v_
                    ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, None, 0, current_stream_ptr(), None)
     check(load().mk_decode_step_noalloc(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def set_grid_size(workgroups: int, device: Optional[int] = None) -> None:
+    """``mk_set_grid_size``: run the kernels on ``workgroups`` workgroups (0:
+    one per CU) for the steps launched after the call."""
+    dev = torch.cuda.current_device() if device is None else device
+    check(load().mk_set_grid_size(dev, workgroups))
+
+
+def grid_size(device: Optional[int] = None) -> int:
+    dev = torch.cuda.current_device() if device is None else device
+    g = load().mk_grid_size(dev)
+    if g < 0:
+        check(g)
+    return g
 
 
 def noalloc_device_error() -> int:
