@@ -3,8 +3,8 @@
 
 Workload ("C3"): random-init bf16 weights (seed 0),
 a 384-token uniform-random prompt prefilled into a 1024-row KV cache on the
-GPU (the batched kernel's prefill step, 32 prompt tokens per launch; its
-latency is reported as prefill_ms), then greedy decode. A *step* is one decode step — one
+GPU (``mk_prefill``: layer by layer on the matrix cores, each layer's weights
+streamed once for the whole prompt; its latency is reported as prefill_ms), then greedy decode. A *step* is one decode step — one
 launch of the persistent megakernel (16 layers + final norm + tied lm_head +
 argmax) for one token; the token and position are fed back on the device, so
 consecutive steps need no host work. W untimed warm-up steps run first, the
@@ -239,7 +239,7 @@ def main():
     model.prefill(prompt)                        # warm-up (first use allocates the prefill workspace)
     torch.cuda.synchronize()
     tp = time.perf_counter()
-    model.prefill(prompt)                        # context encoding: 383 prompt tokens in chunks of 32
+    model.prefill(prompt)                        # context encoding: 383 prompt tokens, layer by layer
     torch.cuda.synchronize()
     prefill_ms = (time.perf_counter() - tp) * 1e3
     if model.prefill_device_error():

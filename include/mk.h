@@ -306,6 +306,54 @@ int mk_decode_step(const mk_weights *w, const mk_step_args *a);
 int mk_decode_step_noalloc(const mk_weights *w, const mk_step_args *a);
 
 /*
+ * Context encoding (prefill) of one sequence: the K/V rows of n_tokens
+ * consecutive prompt tokens at positions start_pos .. start_pos + n_tokens - 1,
+ * written into every requested layer's cache, each token attending causally
+ * to rows [0, its position] (rows below start_pos must hold the sequence's
+ * earlier K/V). Counterpart of the reference's context-encoding pass, which
+ * runs its baseline decoder layers over the prompt (llama_with_megakernel.py:
+ * 194-204; the layer at llama.py:1039-1139), and of mk_decode_step's
+ * MK_FLAG_PREFILL path, which runs at most 32 tokens per launch of the decode
+ * megakernel: this entry point runs layer by layer (RMSNorm, QKV GEMM with
+ * RoPE, causal attention, O GEMM, RMSNorm, gate/up GEMM with SwiGLU, down GEMM)
+ * on the matrix cores, in chunks as large as the workspace holds, so each
+ * layer's weights stream once per chunk. Same rounding points as the decode
+ * step; the attention keeps p = exp(s - running max) rounded to bf16 for the
+ * PV product.
+ *   tokens: device int32 [n_tokens]; k_cache[i] / v_cache[i]: layer
+ *     first_layer + i of ONE sequence, bf16 [8][s_max][64];
+ *     0 <= start_pos, start_pos + n_tokens <= s_max <= rope_rows.
+ *   hidden_out: bf16 [n_tokens][2048], the hidden state after the last layer
+ *     (before the final norm), or NULL (the last layer then runs its QKV
+ *     GEMM only).
+ *   workspace: device memory of at least mk_prefill_workspace_bytes(c)
+ *     bytes, 256-byte aligned, for chunks of c tokens (the entry point takes
+ *     the largest multiple of 16 the given size holds, up to 16384): one
+ *     layer's activations of a chunk (36,864 bytes per token) and a fixed
+ *     16 MiB of fp32 split-K partials; no initialisation, contents not kept
+ *     between calls.
+ *   Uses the MFMA-tiled weight copies when all of t_qkv, t_o, t_gu, t_down
+ *   are set, else the row-major stacks. Asynchronous on `stream`; no
+ *   allocation; every launch is an ordinary kernel (capturable).
+ */
+typedef struct mk_prefill_args {
+    int32_t first_layer;
+    int32_t n_layers;
+    int32_t n_tokens;
+    int32_t start_pos;
+    int32_t s_max;
+    const int32_t *tokens;
+    void *const *k_cache;
+    void *const *v_cache;
+    void *hidden_out;
+    void *workspace;
+    size_t workspace_bytes;
+    void *stream;
+} mk_prefill_args;
+size_t mk_prefill_workspace_bytes(int32_t chunk_tokens);
+int mk_prefill(const mk_weights *w, const mk_prefill_args *a);
+
+/*
  * Single-layer step (transformer_llama_megakernel_1layer,
  * transformer_llama.py:154-191): layer `layer` of the stacks applied to
  * hidden_in, result in hidden_out, K/V row pos[b] written in place.

@@ -68,6 +68,7 @@
 #include "mk.h"
 #include "mk_batch.h"
 #include "mk_common.h"
+#include "mk_prefill.h"
 
 namespace {
 
@@ -1314,6 +1315,43 @@ int mk_decode_step_noalloc(const mk_weights* w, const mk_step_args* a) {
   rc = noalloc_scratch(dev, static_cast<hipStream_t>(a->stream), &base);
   if (rc != MK_OK) return rc;
   return launch_decode(w, a, di, base, base + CTRL_BYTES, true);
+}
+
+size_t mk_prefill_workspace_bytes(int32_t chunk_tokens) {
+  if (chunk_tokens < 1 || chunk_tokens > PREFILL_MAX_CHUNK) return 0;
+  return prefill_ws_bytes(chunk_tokens);
+}
+
+int mk_prefill(const mk_weights* w, const mk_prefill_args* a) {
+  if (!w || !a) return fail(MK_ERR_NULL, "weights or args is NULL");
+  if (a->n_layers < 1 || a->first_layer < 0 || a->first_layer + a->n_layers > w->n_layers ||
+      w->n_layers > MK_MAX_LAYERS)
+    return fail(MK_ERR_SHAPE, "layers [%d, %d) not within the %d packed layers (max %d)", a->first_layer,
+                a->first_layer + a->n_layers, w->n_layers, MK_MAX_LAYERS);
+  if (a->n_tokens < 1) return fail(MK_ERR_SHAPE, "n_tokens %d < 1", a->n_tokens);
+  if (a->start_pos < 0 || a->s_max < 1 || (long long)a->start_pos + a->n_tokens > a->s_max ||
+      a->s_max > w->rope_rows)
+    return fail(MK_ERR_SHAPE, "positions [%d, %d) must lie in [0, s_max=%d], s_max <= rope_rows=%d", a->start_pos,
+                a->start_pos + a->n_tokens, a->s_max, w->rope_rows);
+  if (!a->tokens || !a->k_cache || !a->v_cache) return fail(MK_ERR_NULL, "tokens / k_cache / v_cache is NULL");
+  if (!w->w_qkv || !w->w_o || !w->w_gu || !w->w_down || !w->embed || !w->rope)
+    return fail(MK_ERR_NULL, "a weight pointer is NULL");
+  for (int i = 0; i < a->n_layers; ++i) {
+    if (!a->k_cache[i] || !a->v_cache[i]) return fail(MK_ERR_NULL, "cache pointer of layer %d is NULL", i);
+    if (!aligned16(a->k_cache[i]) || !aligned16(a->v_cache[i]))
+      return fail(MK_ERR_ALIGN, "cache of layer %d not 16-byte aligned", i);
+  }
+  if (!aligned16(a->tokens) || (a->hidden_out && !aligned16(a->hidden_out)))
+    return fail(MK_ERR_ALIGN, "tokens / hidden_out not 16-byte aligned");
+  if (!a->workspace) return fail(MK_ERR_NULL, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(a->workspace) & 255u) return fail(MK_ERR_WORKSPACE, "workspace not 256-byte aligned");
+  const int cap = prefill_chunk_cap(a->workspace_bytes);
+  if (cap < 1)
+    return fail(MK_ERR_WORKSPACE, "workspace %zu bytes < %zu (mk_prefill_workspace_bytes(16))", a->workspace_bytes,
+                prefill_ws_bytes(16));
+  const hipError_t e = prefill_launch(w, a, cap);
+  if (e != hipSuccess) return fail(MK_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+  return MK_OK;
 }
 
 int mk_layer_step(const mk_weights* w, int32_t layer, int32_t batch, int32_t s_max, void* k_cache, void* v_cache,

@@ -21,11 +21,13 @@ Mirrors the reference module ``llama_with_megakernel`` (selected by
 ``model_path`` is a local HF checkpoint directory (safetensors) or
 ``"random:<seed>"`` for the synthetic N(0, 0.02) weights used by the
 benchmarks. Prefill (context encoding, the reference's baseline-layer path at
-llama_with_megakernel.py:194-204) runs the batched MFMA kernel over chunks of
-up to 32 consecutive prompt tokens per launch (``MK_FLAG_PREFILL``: causal
-attention over the cache rows, including the rows of the chunk's own earlier
-tokens); ``prefill(..., batched=False)`` instead runs the decode megakernel
-once per prompt token with logits skipped.
+llama_with_megakernel.py:194-204) runs layer by layer on the matrix cores
+(``mk_prefill``: per layer an RMSNorm, the QKV GEMM with RoPE writing the K/V
+rows, causal attention, the O GEMM, an RMSNorm, the gate/up GEMM with SwiGLU
+and the down GEMM, each layer's weights streamed once per chunk of prompt
+tokens); ``prefill(..., method="chunks")`` runs the batched decode kernel over
+up to 32 consecutive tokens per launch (``MK_FLAG_PREFILL``) and
+``method="tokens"`` the decode megakernel once per prompt token.
 
 TP must be 1, as the reference asserts (llama_with_megakernel.py:147-150).
 """
@@ -264,7 +266,8 @@ class NeuronLlamaForCausalLMMK:
         self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
         self.logits = torch.zeros(B, d.vocab, dtype=torch.float32, device=dev)
         self.hidden_out = torch.zeros(B, d.hidden, dtype=torch.bfloat16, device=dev)
-        self.pf_ws: Optional[mk_lib.Workspace] = None   # batched workspace of the prefill steps (on first use)
+        self.pf_ws: Optional[mk_lib.Workspace] = None   # batched workspace of the 32-token prefill steps (on first use)
+        self.pf_layers_ws: Optional[torch.Tensor] = None  # mk_prefill's workspace (on first use)
         self.ws1: Optional[mk_lib.Workspace] = None     # batch-1 workspace of token-by-token prefill (B > 1)
         self.pf_pos = torch.arange(self.s_max, dtype=torch.int32, device=dev)
         self._ready = True
@@ -372,16 +375,25 @@ class NeuronLlamaForCausalLMMK:
                 raise ValueError(f"prompt of {int(p.numel())} tokens does not fit max_context_length {self.s_max}")
         return ps
 
+    PREFILL_METHODS = ("layers", "chunks", "tokens")
+
     @torch.no_grad()
-    def prefill(self, prompt, batched: bool = True) -> None:
+    def prefill(self, prompt, method: str = "layers", batched: Optional[bool] = None) -> None:
         """For each sequence b, write the K/V rows of its prompt tokens 0..n_b-2
         into its own cache slice; leaves its last prompt token in the token
         buffer and pos[b] = n_b - 1, so the next decode step processes it and
         yields the first generated token.
 
-        batched: chunks of up to 32 consecutive tokens of one sequence per launch
-        of the batched kernel (MK_FLAG_PREFILL); otherwise one decode-kernel
-        launch per token."""
+        method "layers" (default): ``mk_prefill``, layer by layer on the matrix
+        cores, each layer's weights streamed once per chunk of up to 4096
+        tokens; "chunks": launches of the batched decode kernel over up to 32
+        consecutive tokens (MK_FLAG_PREFILL); "tokens": one decode-kernel launch
+        per token. ``batched`` (earlier interface): True = "chunks", False =
+        "tokens"."""
+        if batched is not None:
+            method = "chunks" if batched else "tokens"
+        if method not in self.PREFILL_METHODS:
+            raise ValueError(f"prefill method {method!r} not in {self.PREFILL_METHODS}")
         prompts = self._prompts(prompt)
         self.reset()
         dev = self.pos.device
@@ -390,14 +402,19 @@ class NeuronLlamaForCausalLMMK:
             n = int(p.numel())
             prompt_dev = p.to(device=dev, dtype=torch.int32)
             kc, vc = self.seq_caches(b)
-            if batched:
+            if method == "layers":
+                if n > 1:
+                    if self.pf_layers_ws is None:
+                        self.pf_layers_ws = mk_lib.prefill_workspace(min(self.s_max, 4096), dev)
+                    mk_lib.prefill(self.weights, prompt_dev[:n - 1], kc, vc, 0, self.pf_layers_ws)
+            elif method == "chunks":
                 if self.pf_ws is None:
                     self.pf_ws = mk_lib.Workspace(mk_lib.PREFILL_CHUNK, self.s_max, dev)
                 for c0 in range(0, n - 1, mk_lib.PREFILL_CHUNK):
                     m = min(mk_lib.PREFILL_CHUNK, n - 1 - c0)
                     mk_lib.decode_step(self.weights, self.pf_ws, kc, vc, self.pf_pos[c0:c0 + m],
                                        tokens=prompt_dev[c0:c0 + m], flags=mk_lib.MK_FLAG_PREFILL, batch=m)
-            elif self.batch_size == 1:
+            elif self.batch_size == 1:   # "tokens"
                 pf = self.launcher("prefill")
                 for i in range(n - 1):
                     self.tokens.copy_(prompt_dev[i:i + 1])

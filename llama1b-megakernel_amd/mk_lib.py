@@ -60,6 +60,14 @@ class MkStepArgs(ctypes.Structure):
     ]
 
 
+class MkPrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("first_layer", c_int32), ("n_layers", c_int32), ("n_tokens", c_int32), ("start_pos", c_int32),
+        ("s_max", c_int32), ("tokens", c_void_p), ("k_cache", POINTER(c_void_p)), ("v_cache", POINTER(c_void_p)),
+        ("hidden_out", c_void_p), ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("stream", c_void_p),
+    ]
+
+
 class MkSampleArgs(ctypes.Structure):
     _fields_ = [
         ("logits", c_void_p), ("batch", c_int32), ("vocab", c_int32), ("vocab_stride", c_int32),
@@ -110,6 +118,10 @@ def load() -> ctypes.CDLL:
         lib.mk_layer_step.argtypes = [POINTER(MkWeights), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.mk_layer_step.restype = c_int
+        lib.mk_prefill.argtypes = [POINTER(MkWeights), POINTER(MkPrefillArgs)]
+        lib.mk_prefill.restype = c_int
+        lib.mk_prefill_workspace_bytes.argtypes = [c_int32]
+        lib.mk_prefill_workspace_bytes.restype = c_size_t
         lib.mk_sample.argtypes = [POINTER(MkSampleArgs)]
         lib.mk_sample.restype = c_int
         lib.mk_sample_last_error.restype = c_char_p
@@ -275,6 +287,40 @@ def decode_step_noalloc(weights: MkWeights, k_caches: Sequence[torch.Tensor], v_
                    ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), _ptr(hidden_in), _ptr(pos),
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, None, 0, current_stream_ptr(), None)
     check(load().mk_decode_step_noalloc(ctypes.byref(weights), ctypes.byref(a)))
+
+
+PREFILL_MAX_CHUNK = 16384   # tokens one pass of mk_prefill's layer loop takes at most
+
+
+def prefill_workspace(chunk_tokens: int, device) -> torch.Tensor:
+    """A workspace for ``mk_prefill`` in chunks of up to ``chunk_tokens`` tokens
+    (256-byte aligned device bytes)."""
+    n = load().mk_prefill_workspace_bytes(min(max(int(chunk_tokens), 16), PREFILL_MAX_CHUNK))
+    if n == 0:
+        raise MkError(-2, f"no prefill workspace size for {chunk_tokens} tokens")
+    buf = torch.empty(n, dtype=torch.uint8, device=device)
+    assert buf.data_ptr() % 256 == 0
+    return buf
+
+
+def prefill(weights: MkWeights, tokens: torch.Tensor, k_caches: Sequence[torch.Tensor],
+            v_caches: Sequence[torch.Tensor], start_pos: int, workspace: torch.Tensor, *,
+            hidden_out: Optional[torch.Tensor] = None, first_layer: int = 0,
+            n_layers: Optional[int] = None) -> None:
+    """``mk_prefill`` on the current stream: the K/V rows of ``tokens`` (device
+    int32 [T]) at positions start_pos .. start_pos + T - 1 of one sequence's
+    caches (bf16 [8][S][64] or [1][8][S][64] per layer)."""
+    n = len(k_caches) if n_layers is None else n_layers
+    if len(k_caches) < n or len(v_caches) < n:
+        raise ValueError("need one K and one V cache per layer run")
+    if tokens.dtype != torch.int32 or not tokens.is_contiguous():
+        raise ValueError("tokens must be contiguous int32")
+    kc = (c_void_p * n)(*[t.data_ptr() for t in k_caches[:n]])
+    vc = (c_void_p * n)(*[t.data_ptr() for t in v_caches[:n]])
+    a = MkPrefillArgs(first_layer, n, int(tokens.numel()), int(start_pos), int(k_caches[0].shape[-2]),
+                      tokens.data_ptr(), ctypes.cast(kc, POINTER(c_void_p)), ctypes.cast(vc, POINTER(c_void_p)),
+                      _ptr(hidden_out), workspace.data_ptr(), workspace.numel(), current_stream_ptr())
+    check(load().mk_prefill(ctypes.byref(weights), ctypes.byref(a)))
 
 
 def set_grid_size(workgroups: int, device: Optional[int] = None) -> None:

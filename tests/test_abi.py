@@ -130,3 +130,53 @@ def test_noalloc_step_argument_checks(lib):
     assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -3
     a, keep = _args(workspace=None, workspace_bytes=0, pos=None)
     assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -1
+
+
+def _pf_args(**over):
+    import mk_lib
+    kc = (c_void_p * 16)(*([0x1000] * 16))
+    vc = (c_void_p * 16)(*([0x2000] * 16))
+    a = dict(first_layer=0, n_layers=16, n_tokens=100, start_pos=0, s_max=1024, tokens=0x3000,
+             k_cache=ctypes.cast(kc, POINTER(c_void_p)), v_cache=ctypes.cast(vc, POINTER(c_void_p)),
+             hidden_out=None, workspace=0x100000, workspace_bytes=1 << 24, stream=None)
+    a.update(over)
+    return mk_lib.MkPrefillArgs(**a), (kc, vc)
+
+
+def test_prefill_workspace_size(lib):
+    """mk_prefill_workspace_bytes: linear in the chunk (multiples of 16 tokens), 0 outside [1, 16384]."""
+    assert lib.mk_prefill_workspace_bytes(0) == 0
+    assert lib.mk_prefill_workspace_bytes(16385) == 0
+    assert lib.mk_prefill_workspace_bytes(1) == lib.mk_prefill_workspace_bytes(16)
+    b16, b32 = lib.mk_prefill_workspace_bytes(16), lib.mk_prefill_workspace_bytes(32)
+    per_token = (b32 - b16) // 16
+    assert per_token == 2048 * 2 * 5 + 8192 * 2          # x, h1, q, xn, att (bf16 [2048]) + act (bf16 [8192])
+    assert lib.mk_prefill_workspace_bytes(4096) == b16 + (4096 - 16) * per_token
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(n_layers=0), -2),
+    (dict(first_layer=15, n_layers=2), -2),
+    (dict(n_tokens=0), -2),
+    (dict(start_pos=-1), -2),
+    (dict(start_pos=1000, n_tokens=25), -2),      # past s_max
+    (dict(s_max=9000), -2),                       # beyond the RoPE table
+    (dict(tokens=None), -1),
+    (dict(k_cache=None), -1),
+    (dict(workspace=None), -1),
+    (dict(workspace=0x100010), -3),
+    (dict(workspace_bytes=1000), -3),
+    (dict(tokens=0x3004), -7),
+])
+def test_prefill_rejects_bad_arguments(lib, over, code):
+    a, keep = _pf_args(**over)
+    rc = lib.mk_prefill(ctypes.byref(_weights()), ctypes.byref(a))
+    assert rc == code, (rc, lib.mk_last_error())
+    assert lib.mk_last_error()
+
+
+def test_prefill_rejects_bad_weights(lib):
+    a, keep = _pf_args()
+    assert lib.mk_prefill(ctypes.byref(_weights(w_gu=None)), ctypes.byref(a)) == -1
+    assert lib.mk_prefill(ctypes.byref(_weights(n_layers=8)), ctypes.byref(a)) == -2
+    assert lib.mk_prefill(None, ctypes.byref(a)) == -1
