@@ -21,12 +21,15 @@
 // rows are the prefill's output) unless the caller asks for the hidden state.
 //
 // GEMMs: bf16 v_mfma_f32_16x16x32_bf16 with fp32 accumulation, a 128x128
-// output tile per 256-thread workgroup, 64x64 per wave (16 MFMA tiles). Both
-// operands reach the lanes straight from memory as MFMA operands: the
+// output tile per 256-thread workgroup, 64x64 per wave (16 MFMA tiles). The
 // activations are kept in A-tile order (the producing kernel writes them so)
-// and the weights are the MFMA-tiled copies, so every load is 1 KiB
-// contiguous per wave; the next k-step's operands are in flight while the
-// current one's 16 MFMAs run.
+// and the weights are the MFMA-tiled copies, so each k-step's operands of the
+// tile are 16 blocks of 1 KiB, which the four waves copy from memory straight
+// into LDS (one contiguous 1 KiB copy each, four per wave) three k-steps ahead
+// of their use; each wave reads its 4 A and 4 B operands of a k-step from LDS
+// (a block per instruction, conflict-free) and runs 16 MFMAs. The O and down
+// projections of short prompts (few row tiles) split K across workgroups into
+// fp32 partials that pf_reduce_norm sums in a fixed order.
 //
 // Attention: per (kv head, block of 16 tokens) one workgroup; S^T = K Q^T on
 // the matrix cores (keys on M, the 16 tokens x 4 q heads on N), an online
@@ -66,61 +69,78 @@ struct GemmArgs {
   int s_max, p0;
 };
 
-// One wave's 64x64 block at k-step ks: A tiles m16 = am + i, B tiles
-// n16 = bn + j (i, j < 4); k-steps >= ke read nothing (out-of-range offsets).
-__device__ __forceinline__ void gemm_load(const GemmArgs& g, rsrc_t ra, rsrc_t rb, int am, int bn, int ks, int ke,
-                                          u32x4 (&a)[4], u32x4 (&b)[4]) {
-  const int lane = lane_id(), kb = g.K / 32;
-  const bool kin = ks < ke;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    a[i] = ld16(ra, kin ? (uint32_t)(((size_t)(am + i) * kb + ks) * 1024 + lane * 16) : OOB);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t off = OOB;
-    if (kin) {
-      const int n16 = bn + j;
-      off = g.tiled ? (uint32_t)(((size_t)n16 * kb + ks) * 1024 + lane * 16)
-                    : (uint32_t)((((size_t)n16 * 16 + (lane & 15)) * g.K + ks * 32 + (lane >> 4) * 8) * 2);
-    }
-    b[j] = ld16(rb, off);
-  }
-}
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One k-step of a workgroup's 128x128 tile in LDS: the 8 A blocks (16 rows x
+// 32 columns each, 1 KiB, MFMA A-operand lane order) and the 8 B blocks.
+struct GemmStage {
+  u32x4 a[8][64];
+  u32x4 b[8][64];
+};
+struct GemmLds {
+  GemmStage st[GEMM_NS];
+};
 
 template <int EPI>
 __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
-  const int wave = wave_id(), lane = lane_id();
+  __shared__ GemmLds L;
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();   // (uniform: LDS copy bases)
   const int nbn = g.N / PF_TN;
   const int tm = blockIdx.x / nbn, tn = blockIdx.x % nbn;
-  const int am = (tm * PF_TM + (wave & 1) * 64) / 16;     // first A tile (16 rows) of the wave
-  const int bn = (tn * PF_TN + (wave >> 1) * 64) / 16;    // first B tile (16 columns)
   const int m16 = (g.M + 15) / 16;
   const rsrc_t ra = make_rsrc(g.a, (size_t)m16 * 16 * g.K * 2);
   const rsrc_t rb = make_rsrc(g.b, (size_t)g.N * g.K * 2);
   // the k-steps of this workgroup: all of K, or part blockIdx.y of `splits`
   const int kb = g.K / 32, kn = EPI == EPI_PART ? kb / g.splits : kb;
   const int k0 = EPI == EPI_PART ? (int)blockIdx.y * kn : 0, ke = k0 + kn;   // kn: a multiple of GEMM_NS
+  // Staging: wave w copies A blocks 2w, 2w+1 and B blocks 2w, 2w+1 of each
+  // k-step from memory straight into LDS (one 1 KiB copy each); k-steps
+  // >= ke copy zeros from out-of-range offsets (no memory read).
+  const int ab0 = tm * 8 + 2 * wave, bb0 = tn * 8 + 2 * wave;
+  auto issue = [&](int ks, int stg) {
+    const bool kin = ks < ke;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t ao = kin ? (uint32_t)(((size_t)(ab0 + u) * kb + ks) * 1024 + lane * 16) : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&L.st[stg].a[2 * wave + u][0], 16, ao, 0, 0, 0);
+      uint32_t bo = OOB;
+      if (kin)
+        bo = g.tiled ? (uint32_t)(((size_t)(bb0 + u) * kb + ks) * 1024 + lane * 16)
+                     : (uint32_t)((((size_t)(bb0 + u) * 16 + (lane & 15)) * g.K + ks * 32 + (lane >> 4) * 8) * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&L.st[stg].b[2 * wave + u][0], 16, bo, 0, 0, 0);
+    }
+  };
+  // wave (wm, wn) computes rows 64*wm .. +63 and columns 64*wn .. +63 of the tile
+  const int wm = wave & 1, wn = wave >> 1;
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // a ring of GEMM_NS operand stages: the loads of the next GEMM_NS - 1
-  // k-steps are in flight while one k-step's 16 MFMAs run
-  u32x4 ar[GEMM_NS][4], br[GEMM_NS][4];
 #pragma unroll
-  for (int s = 0; s < GEMM_NS - 1; ++s) gemm_load(g, ra, rb, am, bn, k0 + s, ke, ar[s], br[s]);
+  for (int s = 0; s < GEMM_NS - 1; ++s) issue(k0 + s, s);
   for (int ks = k0; ks < ke; ks += GEMM_NS) {
 #pragma unroll
     for (int s = 0; s < GEMM_NS; ++s) {
-      const int nx = (s + GEMM_NS - 1) % GEMM_NS;
-      gemm_load(g, ra, rb, am, bn, ks + s + GEMM_NS - 1, ke, ar[nx], br[nx]);   // past ke: nothing read
+      // this wave's copies of stage s have landed (the GEMM_NS - 2 later
+      // stages' 4 copies each may be in flight), and, after the barrier, every
+      // wave's; every wave has also finished reading the stage refilled next
+      static_assert(GEMM_NS == 4, "the wait below counts 2 later stages of 4 copies");
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+      issue(ks + s + GEMM_NS - 1, (s + GEMM_NS - 1) % GEMM_NS);
+      const GemmStage& S = L.st[s];
+      u32x4 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = S.a[4 * wm + i][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = S.b[4 * wn + j][lane];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(ar[s][i], br[s][j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(av[i], bv[j], acc[i][j]);
     }
   }
+  const int am = tm * 8 + 4 * wm, bn = tn * 8 + 4 * wn;   // the wave's first A / B tile
 
   // epilogue: acc[i][j][r] is (row 16*(am+i) + 4*(lane/16) + r, column 16*(bn+j) + lane%16)
 #pragma unroll
