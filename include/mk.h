@@ -175,7 +175,10 @@ typedef struct mk_step_args {
      * lm_head input. Slot MK_TRACE_DONE0 + 5*i + j (below MK_TRACE_SLOTS-8)
      * is recorded when phase j (0 QKV, 1 attention, 2 O, 3 gate/up, 4 down)
      * of run-layer i has issued its result stores; slots MK_TRACE_SLOTS-8 ..
-     * MK_TRACE_SLOTS-2 hold kernel-specific diagnostic values. */
+     * MK_TRACE_SLOTS-2 hold kernel-specific diagnostic values (in a decode
+     * loop, whose trace keeps the marks of its last step: MK_TRACE_SLOTS-4 the
+     * previous step's arrival at the step barrier, -3 the barrier seen, -2
+     * the token read). */
     void *trace;
 } mk_step_args;
 
@@ -276,6 +279,32 @@ int mk_read_device_error(void *workspace, void *stream, uint32_t *bits_out);
 
 /* The decode step (see mk_step_args). Asynchronous on the stream. */
 int mk_decode_step(const mk_weights *w, const mk_step_args *a);
+
+/*
+ * Greedy decode loop: n_steps consecutive batch-1 decode steps in ONE
+ * persistent launch, each step's token the previous step's argmax. No
+ * counterpart in the reference, whose generation loop (NxDI, main.py:178-271)
+ * launches one token-generation step per token; mk_decode_step is that seam.
+ * Between steps the workgroups meet at an on-device barrier instead of a
+ * kernel boundary, so the next step's layer-0 weights stream while the
+ * slowest workgroups finish the lm_head, and no launch gap separates the
+ * steps. Each step is the mk_decode_step computation (bitwise: same kernel
+ * code, rows, order and rounding).
+ *   a: as for mk_decode_step with batch 1, tokens[0] the first step's token
+ *     (hidden_in must be NULL), a batch-1 workspace; positions pos[0] ..
+ *     pos[0] + n_steps - 1 must lie below s_max and rope_rows; logits (if
+ *     given) receive the last step's, next_token (if given) the last step's
+ *     token; MK_FLAG_ADVANCE advances pos by n_steps.
+ *   tokens_out: device int32 [n_steps], the token each step produced, or NULL.
+ *   step_clock: device uint64 [n_steps + 1], or NULL: the device wall clock
+ *     (mk_wall_clock_hz) at the launch's start, when step n's token was known
+ *     to workgroup 0 (entry n + 1, n < n_steps - 1), and when the launch
+ *     ended (entry n_steps): entry differences are per-step latencies.
+ *   MK_ERR_UNSUPPORTED for batch > 1, hidden_in, MK_FLAG_PREFILL or a batched
+ *   workspace. Asynchronous on the stream; allocates nothing.
+ */
+int mk_decode_loop(const mk_weights *w, const mk_step_args *a, int32_t n_steps, int32_t *tokens_out,
+                   uint64_t *step_clock);
 
 /*
  * Allocation-free variant of mk_decode_step. No counterpart in the reference:

@@ -103,7 +103,13 @@ constexpr int MAX_GRID = 1024;
 constexpr size_t CTRL_BYTES = 256;
 constexpr int C_EXIT = 0, C_ERR = 1, C_EPOCH = 2;   // u32 words of the control block
 constexpr int C_STICKY = 3;   // allocation-free scratch only: error bits of every faulted step since the last read
-constexpr size_t C_KEY_BYTE = 128;                  // u64 argmax key
+constexpr size_t C_KEY_BYTE = 128;                  // u64 argmax key (a decode loop alternates it
+                                                    // with C_KEY_BYTE + 64 by step parity)
+// Decode loop (several steps in one launch): step-barrier sub-counters, one
+// 128-byte line each, in the workspace's exchange area after the two sets.
+constexpr int STEP_LINES = 32;
+constexpr size_t STEP_LINE = 128;
+constexpr size_t STEP_CNT_BYTES = (size_t)STEP_LINES * STEP_LINE;
 // Exchange buffers of one layer; each region starts on a 256-byte boundary.
 constexpr size_t X_QKV = 0;                                 // bf16 q[2048] | k[512] | v[512]
 constexpr size_t X_K = (size_t)NQ * HD * 2, X_V = X_K + (size_t)NKV * HD * 2;   // within X_QKV
@@ -148,6 +154,10 @@ struct KParams {
   uint32_t flags;
   unsigned long long timeout_ticks;
   unsigned long long* trace;
+  int n_steps;                      // decode steps of this launch (a greedy loop when > 1)
+  int32_t* tokens_out;              // [n_steps] each step's greedy token, or NULL
+  unsigned long long* step_clock;   // [n_steps + 1] device wall clock at the step boundaries, or NULL
+  uint32_t* step_cnt;               // loop: the step-barrier sub-counters (STEP_LINES lines)
 };
 
 // ---------------------------------------------------------------------------
@@ -415,10 +425,16 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, R
       uint16_t* dst = xq + (is_k ? X_K : X_V) / 2 + kh * HD + d;
       st_dev(dst, o.x);
       st_dev(dst + 32, o.y);
-      // the cache row is read only by later launches: a plain store
+      // the cache row: read by later launches (a plain store), or, in a decode
+      // loop, by the next step of this launch on any XCD (a device-scope store)
       uint16_t* crow = (is_k ? kcl : vcl) + ((size_t)kh * p.s_max + c.pos) * HD + d;
-      crow[0] = (uint16_t)o.x;
-      crow[32] = (uint16_t)o.y;
+      if (p.n_steps > 1) {
+        st_dev(crow, o.x);
+        st_dev(crow + 32, o.y);
+      } else {
+        crow[0] = (uint16_t)o.x;
+        crow[32] = (uint16_t)o.y;
+      }
     }
   }
   trace_done(c.s, li, 0);
@@ -476,6 +492,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   c.s.timeout = p.timeout_ticks;
   c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
   trace_mark(c.s, 0);
+  if (p.step_clock && blockIdx.x == 0 && threadIdx.x == 0) p.step_clock[0] = wall_clock64();
   c.G = GFIX ? GFIX : (int)gridDim.x;
   c.w = blockIdx.x;
   // The control words, the position and the token first; then the first
@@ -490,17 +507,19 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   RowStream<4, 4> qs;   // the QKV ring of the layer being run
   qkv_ring(c, 0, qs);
   c.set = p.xch + (size_t)(epoch & 1u) * SET_BYTES;
-  // refill the other set with the sentinel for the next launch: during the
-  // lm_head phase, where the stores delay nothing, or here if there is none
-  auto refill = [&]() {
-    u32x4* other = reinterpret_cast<u32x4*>(p.xch + (size_t)((epoch + 1u) & 1u) * SET_BYTES);
+  // refill the other set with the sentinel for the next step: during the
+  // lm_head phase of step n, where the stores delay nothing, or here if there
+  // is none (step n uses set (epoch + n) & 1)
+  auto refill = [&](int step) {
+    u32x4* other = reinterpret_cast<u32x4*>(p.xch + (size_t)((epoch + (uint32_t)step + 1u) & 1u) * SET_BYTES);
     const size_t n = SET_BYTES / 16;
     int lo, hi;
     share((int)n, c.G, c.w, lo, hi);
     for (int i = lo + threadIdx.x; i < hi; i += NT) other[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   };
-  const bool pos_ok = c.pos >= 0 && c.pos < p.s_max && c.pos < p.rope_rows;
-  if (!p.do_lm || !pos_ok) refill();   // (the lm_head phase runs only with a valid position)
+  const int pos0 = c.pos;   // a loop's step n runs at position pos0 + n
+  const bool pos_ok = c.pos >= 0 && c.pos + p.n_steps <= p.s_max && c.pos + p.n_steps <= p.rope_rows;
+  if (!p.do_lm || !pos_ok) refill(0);   // (the lm_head phase runs only with a valid position)
   if (!pos_ok && blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   c.n_rows = c.pos + 1;
@@ -510,12 +529,46 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     tok = tok < 0 ? 0 : (tok >= VOCAB ? VOCAB - 1 : tok);
     c.x_in = p.embed + (size_t)tok * H;
   }
-  // the step's RoPE row, read once; it goes to LDS with the first layer's input
-  uint32_t rope_v = 0;
-  if (pos_ok && threadIdx.x < HD)
-    rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
+  // Decode loop: step n (> 0) starts when every workgroup has finished step
+  // n - 1 (arrivals on STEP_LINES sub-counters) and its greedy token is in
+  // the argmax key of that step's parity; its layer-0 QKV weights are already
+  // in flight, and idle() (the layer-0 gate/up LDS copies) runs between polls.
+  auto key_ptr = [&](int n) { return reinterpret_cast<unsigned long long*>(p.ws + C_KEY_BYTE + 64 * (n & 1)); };
+  auto step_entry = [&](int n, auto&& idle) {
+    const uint32_t per = (uint32_t)(G / STEP_LINES), extra = (uint32_t)(G % STEP_LINES);
+    const rsrc_t r = make_rsrc(p.step_cnt, STEP_CNT_BYTES);
+    const uint32_t off = lane < STEP_LINES ? (uint32_t)lane * (uint32_t)STEP_LINE : OOB;
+    const uint32_t target = lane < STEP_LINES ? (uint32_t)n * (per + ((uint32_t)lane < extra ? 1u : 0u)) : 0u;
+    const unsigned long long t0 = wall_clock64();
+    for (int it = 1;; ++it) {
+      const uint32_t v = ld_dev4(r, off);
+      if (__all(v >= target)) break;
+      if (wait_expired(c.s, t0, it)) break;
+      idle();
+      __builtin_amdgcn_s_sleep(1);
+    }
+    trace_mark(c.s, MK_TRACE_SLOTS - 3);   // (a loop's trace keeps its last step: this step's barrier seen)
+    const unsigned long long key = __hip_atomic_load(key_ptr(n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    trace_mark(c.s, MK_TRACE_SLOTS - 2);
+    int t = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+    if (w == 0 && threadIdx.x == 0) {
+      if (p.tokens_out) p.tokens_out[n - 1] = t;
+      if (p.step_clock) p.step_clock[n] = wall_clock64();
+    }
+    t = t < 0 ? 0 : (t >= VOCAB ? VOCAB - 1 : t);
+    c.x_in = p.embed + (size_t)t * H;
+  };
 
-  if (pos_ok) {
+  if (pos_ok) for (int n = 0; n < p.n_steps; ++n) {
+    const bool last_step = n + 1 == p.n_steps;
+    if (n > 0) {
+      c.pos = pos0 + n;
+      c.n_rows = c.pos + 1;
+      c.set = p.xch + (size_t)((epoch + (uint32_t)n) & 1u) * SET_BYTES;
+    }
+    // the step's RoPE row, read once; it goes to LDS with the first layer's input
+    uint32_t rope_v = 0;
+    if (threadIdx.x < HD) rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
     {
       attn_split(c.n_rows, ATT_MAX_SPLIT, 32, c.nsplit, c.att_rows);
       int R0, R1;
@@ -547,6 +600,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
       if (li > 0) qkv_ring(c, li, qs);
+      if (li == 0 && n > 0) step_entry(n, gidle);
       phase_qkv(c, li, L, gidle, qs, [&]() {
         if (li == 0 && threadIdx.x < HD) reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] = rope_v;
       });
@@ -711,7 +765,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           const int row = sp.lo + r;
           const uint32_t hv = f2bf(bf2f(L.h1[row]) + rbf(v));
           st_dev(h2 + row, hv);
-          if (last && p.hidden_out) p.hidden_out[row] = (uint16_t)hv;
+          if (last && last_step && p.hidden_out) p.hidden_out[row] = (uint16_t)hv;
         };
         if (sp.n <= 2) {   // lanes 0-31: row 0, lanes 32-63: row 1
           float pt[2];
@@ -748,7 +802,11 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       stage_vec<1>(c.s, c.xb(p.n_layers - 1, X_H2), true, L.x);
       lds_sync();
       trace_mark(c.s, 2 * xk(p.n_layers, 1));
-      refill();
+      refill(n);
+      // the next step's argmax key (read by every workgroup at the start of
+      // this step, all of which have passed their first hand-overs by now)
+      if (!last_step && w == 0 && threadIdx.x == 0)
+        __hip_atomic_store(key_ptr(n + 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       u32x4 xs[4];
       lds_x2048(L.x, xs);
       rmsnorm2048(xs, p.g_final);
@@ -758,7 +816,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
              [&](int r, float part) {
                const float v = wave_sum(part);
                const int row = sp.lo + r;
-               if (lane == 0 && p.logits) p.logits[row] = v;
+               if (lane == 0 && p.logits && last_step) p.logits[row] = v;
                if (v > best) {   // rows ascend: keeps the lowest index among equal maxima
                  best = v;
                  bidx = row;
@@ -782,10 +840,21 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
           u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);   // order-preserving float key
           const unsigned long long key =
               ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)bi);
-          __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(p.ws + C_KEY_BYTE), key,
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_max(key_ptr(n), key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
+    }
+    if (!last_step) {
+      // this workgroup's step is complete (its stores, the K/V rows included,
+      // and its argmax contribution): one arrival; then the next step's
+      // layer-0 QKV weights go in flight
+      wait_mem();
+      __syncthreads();
+      trace_mark(c.s, MK_TRACE_SLOTS - 4);   // the step's arrival
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(p.step_cnt + (size_t)(w % STEP_LINES) * (STEP_LINE / 4), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      qkv_ring(c, 0, qs);
     }
   }
 
@@ -800,12 +869,18 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   __syncthreads();
   if (!L.last || threadIdx.x != 0) return;
   ctrl[C_EXIT] = 0u;
-  ctrl[C_EPOCH] = epoch + 1u;
+  ctrl[C_EPOCH] = epoch + (pos_ok ? (uint32_t)p.n_steps : 1u);
   unsigned long long key = 0ull;
   if (pos_ok && p.do_lm) {
-    unsigned long long* kp = reinterpret_cast<unsigned long long*>(p.ws + C_KEY_BYTE);
+    unsigned long long* kp = key_ptr(p.n_steps - 1);
     key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *kp = 0ull;
+  }
+  if (p.n_steps > 1) {   // a loop: both keys and the step counters start the next launch at zero
+    *key_ptr(p.n_steps) = 0ull;
+    for (int j = 0; j < STEP_LINES; ++j) p.step_cnt[(size_t)j * (STEP_LINE / 4)] = 0u;
+    if (p.step_clock) p.step_clock[p.n_steps] = wall_clock64();
+    if (pos_ok && p.tokens_out) p.tokens_out[p.n_steps - 1] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   }
   if (p.noalloc) {
     // In the static scratch the step's error bits are cleared so the next
@@ -955,7 +1030,7 @@ bool exchange_of(const void* ws, int dev, XchEntry* out) {
 
 int exchange_create(const void* ws, int dev, int max_batch, XchEntry* out) {
   const bool uncached = max_batch == 1;
-  size_t need = XCH_BYTES;
+  size_t need = XCH_BYTES + STEP_CNT_BYTES;   // batch 1: the two sets, then the decode loop's step counters
   if (!uncached) {
     BatchLayout lay;
     lay.init(max_batch);
@@ -1055,8 +1130,8 @@ int check_step_args(const mk_weights* w, const mk_step_args* a) {
 
 // Enqueue mk_decode_kernel (batch 1) with control block `ctrl` and exchange sets `xch`.
 int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& di, uint8_t* ctrl, uint8_t* xch,
-                  bool noalloc) {
-  const bool do_lm = a->logits != nullptr || a->next_token != nullptr;
+                  bool noalloc, int n_steps = 1, int32_t* tokens_out = nullptr, uint64_t* step_clock = nullptr) {
+  const bool do_lm = a->logits != nullptr || a->next_token != nullptr || n_steps > 1;
   KParams kp;
   memset(&kp, 0, sizeof(kp));
   kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
@@ -1087,6 +1162,10 @@ int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& 
   kp.flags = a->flags;
   kp.timeout_ticks = di.ticks_per_s * 2ull;   // 2 s per hand-over wait
   kp.trace = static_cast<unsigned long long*>(a->trace);
+  kp.n_steps = n_steps;
+  kp.tokens_out = tokens_out;
+  kp.step_clock = reinterpret_cast<unsigned long long*>(step_clock);
+  kp.step_cnt = n_steps > 1 ? reinterpret_cast<uint32_t*>(xch + XCH_BYTES) : nullptr;
 
   void* args[] = {&kp};
   // One workgroup per CU with occupancy 1 (checked in device_info): on an
@@ -1204,6 +1283,8 @@ int mk_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
   if (xe.max_batch == 1) {   // batch-1 exchange sets start filled with the sentinel
     hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(xe.xch),
                        XCH_BYTES / 16, (size_t)0);
+    hipLaunchKernelGGL(mk_ws_init_kernel, dim3(1), dim3(256), 0, st, reinterpret_cast<u32x4*>(xe.xch + XCH_BYTES),
+                       STEP_CNT_BYTES / 16, STEP_CNT_BYTES / 16);   // the step counters start at zero
   } else {                   // so do the two sentinel sets of a batched exchange area
     BatchLayout lay;
     lay.init(xe.max_batch);
@@ -1294,6 +1375,33 @@ int mk_decode_step(const mk_weights* w, const mk_step_args* a) {
     return MK_OK;
   }
   return launch_decode(w, a, di, static_cast<uint8_t*>(a->workspace), xe.xch, false);
+}
+
+int mk_decode_loop(const mk_weights* w, const mk_step_args* a, int32_t n_steps, int32_t* tokens_out,
+                   uint64_t* step_clock) {
+  int rc = check_step_args(w, a);
+  if (rc != MK_OK) return rc;
+  if (n_steps < 1 || n_steps > (1 << 20)) return fail(MK_ERR_SHAPE, "n_steps %d not in [1, 2^20]", n_steps);
+  if (a->batch != 1) return fail(MK_ERR_UNSUPPORTED, "the decode loop runs batch 1 (batch %d)", a->batch);
+  if (!a->tokens || a->hidden_in)
+    return fail(MK_ERR_UNSUPPORTED, "the decode loop takes token input (each step's token is the last one's argmax)");
+  if (a->flags & MK_FLAG_PREFILL) return fail(MK_ERR_UNSUPPORTED, "MK_FLAG_PREFILL is not a decode loop");
+  if ((tokens_out && !aligned16(tokens_out)) || (step_clock && !aligned16(step_clock)))
+    return fail(MK_ERR_ALIGN, "tokens_out / step_clock not 16-byte aligned");
+  if (!a->workspace) return fail(MK_ERR_NULL, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(a->workspace) & 255u) return fail(MK_ERR_WORKSPACE, "workspace not 256-byte aligned");
+  if (a->workspace_bytes < mk_workspace_bytes(1, a->s_max))
+    return fail(MK_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", a->workspace_bytes, mk_workspace_bytes(1, a->s_max));
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(MK_ERR_HIP, "hipGetDevice failed");
+  DeviceInfo di;
+  rc = device_info(dev, &di);
+  if (rc != MK_OK) return rc;
+  XchEntry xe;
+  if (!exchange_of(a->workspace, dev, &xe))
+    return fail(MK_ERR_WORKSPACE, "workspace was not initialised with mk_workspace_init on device %d", dev);
+  if (xe.max_batch != 1) return fail(MK_ERR_UNSUPPORTED, "the decode loop needs a batch-1 workspace");
+  return launch_decode(w, a, di, static_cast<uint8_t*>(a->workspace), xe.xch, false, n_steps, tokens_out, step_clock);
 }
 
 int mk_decode_step_noalloc(const mk_weights* w, const mk_step_args* a) {

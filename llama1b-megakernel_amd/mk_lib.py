@@ -113,6 +113,8 @@ def load() -> ctypes.CDLL:
         lib.mk_read_device_error.restype = c_int
         lib.mk_decode_step.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
         lib.mk_decode_step.restype = c_int
+        lib.mk_decode_loop.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs), c_int32, c_void_p, c_void_p]
+        lib.mk_decode_loop.restype = c_int
         lib.mk_decode_step_noalloc.argtypes = [POINTER(MkWeights), POINTER(MkStepArgs)]
         lib.mk_decode_step_noalloc.restype = c_int
         lib.mk_layer_step.argtypes = [POINTER(MkWeights), c_int32, c_int32, c_int32, c_void_p, c_void_p,
@@ -269,6 +271,24 @@ def decode_step(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tens
                    _ptr(hidden_out), _ptr(logits), _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes,
                    current_stream_ptr(), _ptr(trace))
     check(load().mk_decode_step(ctypes.byref(weights), ctypes.byref(a)))
+
+
+def decode_loop(weights: MkWeights, ws: Workspace, k_caches: Sequence[torch.Tensor],
+                v_caches: Sequence[torch.Tensor], pos: torch.Tensor, tokens: torch.Tensor, n_steps: int, *,
+                tokens_out: Optional[torch.Tensor] = None, step_clock: Optional[torch.Tensor] = None,
+                logits: Optional[torch.Tensor] = None, next_token: Optional[torch.Tensor] = None,
+                hidden_out: Optional[torch.Tensor] = None, flags: int = 0) -> None:
+    """``mk_decode_loop`` on the current torch stream: ``n_steps`` greedy batch-1
+    decode steps in one launch (tokens_out: int32 [n_steps]; step_clock:
+    int64 [n_steps + 1] device wall-clock ticks at the step boundaries)."""
+    n = len(k_caches)
+    kc = (c_void_p * n)(*[t.data_ptr() for t in k_caches])
+    vc = (c_void_p * n)(*[t.data_ptr() for t in v_caches])
+    a = MkStepArgs(0, n, 1, int(k_caches[0].shape[-2]), ctypes.cast(kc, POINTER(c_void_p)),
+                   ctypes.cast(vc, POINTER(c_void_p)), _ptr(tokens), None, _ptr(pos), _ptr(hidden_out), _ptr(logits),
+                   _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes, current_stream_ptr(), None)
+    check(load().mk_decode_loop(ctypes.byref(weights), ctypes.byref(a), int(n_steps), _ptr(tokens_out),
+                                _ptr(step_clock)))
 
 
 def decode_step_noalloc(weights: MkWeights, k_caches: Sequence[torch.Tensor], v_caches: Sequence[torch.Tensor],

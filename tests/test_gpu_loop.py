@@ -1,0 +1,135 @@
+"""The greedy decode loop (``mk_decode_loop``): several decode steps in one
+persistent launch, the workgroups meeting at an on-device barrier between
+steps, against the same steps launched one by one (``mk_decode_step``).
+
+Each step of the loop is the single step's computation, so from the same
+state (a 64-token prompt prefilled into a 256-row cache) the loop's tokens,
+its last step's logits and hidden state, every K/V cache byte and the advanced
+position equal those of 24 single launches bit for bit. A loop followed by
+single steps continues the exchange-set and argmax-key state (equal to the
+same number of single steps). The step clock is monotonic. Refusals: batch > 1
+workspace, hidden input, and positions past the cache (a device error, nothing
+written).
+"""
+
+import pytest
+import torch
+
+from gpu_common import need_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+S = 256
+N = 24
+
+
+@pytest.fixture(scope="module")
+def model():
+    need_gpu()
+    from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
+    m = NeuronLlamaForCausalLM("random:0", LlamaInferenceConfig(NeuronConfigLlamaMK(seq_len=S)))
+    m.compile()
+    m.load()
+    return m
+
+
+def snapshot(m):
+    torch.cuda.synchronize()
+    return dict(kv=m.kv.clone(), pos=m.pos.clone(), tok=m.tokens.clone())
+
+
+def restore(m, st):
+    m.kv.copy_(st["kv"])
+    m.pos.copy_(st["pos"])
+    m.tokens.copy_(st["tok"])
+    m.logits.zero_()
+    m.hidden_out.zero_()
+    torch.cuda.synchronize()
+
+
+def singles(m, n):
+    dec = m.launcher("decode")
+    toks = []
+    for _ in range(n):
+        dec.launch()
+        toks.append(m.tokens.clone())
+    torch.cuda.synchronize()
+    assert m.ws.read_device_error() == 0
+    return torch.cat(toks).cpu()
+
+
+def loop(m, n, clock=None):
+    import mk_lib
+    out = torch.full((n,), -5, dtype=torch.int32, device="cuda")
+    mk_lib.decode_loop(m.weights, m.ws, m.k_caches, m.v_caches, m.pos, m.tokens, n, tokens_out=out,
+                       step_clock=clock, logits=m.logits, next_token=m.tokens, hidden_out=m.hidden_out,
+                       flags=mk_lib.MK_FLAG_ADVANCE)
+    torch.cuda.synchronize()
+    assert m.ws.read_device_error() == 0
+    return out.cpu()
+
+
+def test_loop_equals_single_steps(model):
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(64, seed=41))
+    st = snapshot(m)
+    ref_toks = singles(m, N)
+    ref = dict(kv=m.kv.clone(), pos=m.pos.clone(), logits=m.logits.clone(), hid=m.hidden_out.clone(),
+               tok=m.tokens.clone())
+    restore(m, st)
+    clock = torch.zeros(N + 1, dtype=torch.int64, device="cuda")
+    got = loop(m, N, clock)
+    say(f"[loop] tokens {got[:8].tolist()}... single steps {ref_toks[:8].tolist()}...")
+    assert torch.equal(got, ref_toks)
+    assert torch.equal(m.tokens, ref["tok"]) and int(m.pos.item()) == int(st["pos"].item()) + N
+    assert torch.equal(m.logits.view(torch.int32), ref["logits"].view(torch.int32))
+    assert torch.equal(m.hidden_out.view(torch.int16), ref["hid"].view(torch.int16))
+    assert torch.equal(m.kv.view(torch.int16), ref["kv"].view(torch.int16))
+    c = clock.cpu()
+    assert bool((c[1:] > c[:-1]).all()), c.tolist()
+    import mk_lib
+    hz = mk_lib.load().mk_wall_clock_hz(0)
+    d = (c[1:] - c[:-1]).double() * 1e6 / hz
+    say(f"[loop] step durations (us): median {float(d.median()):.1f}, min {float(d.min()):.1f}, max {float(d.max()):.1f}")
+
+
+def test_loop_then_single_steps_continue(model):
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(40, seed=43))
+    st = snapshot(m)
+    ref_toks = singles(m, 9)
+    ref_kv = m.kv.clone()
+    restore(m, st)
+    got = torch.cat([loop(m, 5), singles(m, 2), loop(m, 2)])
+    assert torch.equal(got, ref_toks)
+    assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
+
+
+def test_loop_refusals(model):
+    import mk_lib
+    m = model
+    with pytest.raises(mk_lib.MkError) as e:   # hidden input
+        a = m.launcher("decode").args
+        a_hidden = mk_lib.MkStepArgs.from_buffer_copy(a)
+        a_hidden.hidden_in = m.hidden_out.data_ptr()
+        a_hidden.tokens = None
+        mk_lib.check(mk_lib.load().mk_decode_loop(mk_lib.ctypes.byref(m.weights), mk_lib.ctypes.byref(a_hidden),
+                                                  4, None, None))
+    assert e.value.code == -4
+    ws8 = mk_lib.Workspace(8, S, torch.device("cuda"))
+    with pytest.raises(mk_lib.MkError) as e:   # batched workspace
+        mk_lib.decode_loop(m.weights, ws8, m.k_caches, m.v_caches, m.pos, m.tokens, 4)
+    assert e.value.code == -4
+    # positions past the cache: refused on the device, nothing written
+    m.pos.fill_(S - 3)
+    kv0 = m.kv.clone()
+    mk_lib.decode_loop(m.weights, m.ws, m.k_caches, m.v_caches, m.pos, m.tokens, 4, flags=mk_lib.MK_FLAG_ADVANCE)
+    torch.cuda.synchronize()
+    assert m.ws.read_device_error() & mk_lib.MK_DEVERR_POS
+    assert int(m.pos.item()) == S - 3
+    assert torch.equal(m.kv.view(torch.int16), kv0.view(torch.int16))
+    # and the workspace is still good for a loop afterwards
+    m.pos.fill_(10)
+    loop(m, 3)
