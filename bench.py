@@ -4,18 +4,28 @@
 Workload ("C3"): random-init bf16 weights (seed 0),
 a 384-token uniform-random prompt prefilled into a 1024-row KV cache on the
 GPU (``mk_prefill``: layer by layer on the matrix cores, each layer's weights
-streamed once for the whole prompt; its latency is reported as prefill_ms), then greedy decode. A *step* is one decode step — one
-launch of the persistent megakernel (16 layers + final norm + tied lm_head +
-argmax) for one token; the token and position are fed back on the device, so
-consecutive steps need no host work. W untimed warm-up steps run first, the
-state is rewound, and exactly K steps are timed from position 384 (K <= 640,
-so the timed steps cover KV lengths 384..384+K-1).
+streamed once for the whole prompt; its latency is reported as prefill_ms),
+then greedy decode. A *step* is one decode step — 16 layers + final norm + tied
+lm_head + argmax of the persistent megakernel for one token, the token and
+position fed back on the device. One step at position 383 gives the first
+token; then K steps are timed from position 384 (K <= 640, so the timed steps
+cover KV lengths 384..384+K-1), each way the library runs them:
+
+* loop (the headline ``value``): all K steps in ONE launch of the kernel
+  (``mk_decode_loop``, what ``model.generate`` runs for greedy batch 1): an
+  on-device step barrier, each step's argmax read by the next; after a
+  warm-up loop of W steps and a rewind of the state. Step latencies p50/p90
+  from the device wall clock at the step boundaries;
+* launch (``per_launch``): one launch per step, W warm-up launches, K back to
+  back, then the same K again with a HIP event after each for the latency
+  percentiles. The loop's last token and logits must equal the K launches'
+  (the steps are bitwise the same), or the run fails.
 
 Printed (one JSON line on stdout): tok/s over the timed region (host clock,
-synchronised on both sides), ms per step, p50/p90 step latency from HIP events
-on the kernel's stream, the HBM roofline of the megakernel (algorithmic bytes
-per step / mean step time vs 8 TB/s), and a CPU baseline: the oracle's fp32
-decode step timed on this host's cores on a bounded sample.
+synchronised on both sides), ms per step, p50/p90 step latency, the HBM
+roofline of the megakernel (algorithmic bytes per step / mean step time from
+HIP events around the timed launches, vs 8 TB/s), and a CPU baseline: the
+oracle's fp32 decode step timed on this host's cores on a bounded sample.
 
 ``--config c4`` / ``--config c5`` time the batched step instead (BASELINE
 configs 4 and 5; not the headline line). C4: batch 8 through the model seam
@@ -196,6 +206,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=48, help="C3 CPU baseline steps (>= 32)")
     ap.add_argument("--cpu-budget-s", type=float, default=30.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--c3-mode", choices=["loop", "launch", "both"], default="both",
+                    help="C3 steps as one mk_decode_loop launch (loop), one launch per step (launch), or both "
+                         "(the loop is the headline; the per-launch figures go to per_launch)")
     ap.add_argument("--config", choices=["c2", "c3", "c4", "c5"], default="c3",
                     help="c3: the headline bs=1 decode; c2: one decoder layer; c4/c5: the batched configurations")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -251,8 +264,9 @@ def main():
     tok0 = model.tokens.clone()
     assert int(pos0.item()) == PROMPT
 
-    for _ in range(args.warmup):
-        dec.launch()
+    if args.c3_mode != "loop":
+        for _ in range(args.warmup):
+            dec.launch()
     torch.cuda.synchronize()
     model.pos.copy_(pos0)
     model.tokens.copy_(tok0)
@@ -265,25 +279,68 @@ def main():
         model.tokens.copy_(tok0)
         torch.cuda.synchronize()
 
-    wall, mean_ms = timed_steps(dec.launch, K)
-    step_ms = step_latencies(dec.launch, K, reset)
+    per_launch = None
+    if args.c3_mode in ("launch", "both"):
+        # one launch per step (the reference's call pattern): K back-to-back
+        # launches, then the same K again with an event after each for the
+        # latency percentiles
+        wall1, mean1 = timed_steps(dec.launch, K)
+        ref_state = (model.tokens.clone(), model.logits.clone())
+        step_ms1 = step_latencies(dec.launch, K, reset)
+        per_launch = {"value": round(K / wall1, 2), "ms_per_step": round(wall1 * 1e3 / K, 4),
+                      "p50_step_ms": round(statistics.median(step_ms1), 4),
+                      "p90_step_ms": round(sorted(step_ms1)[int(0.9 * (K - 1))], 4),
+                      "kernel_ms_per_step": round(mean1, 4)}
+    loop = None
+    if args.c3_mode in ("loop", "both"):
+        # the greedy loop: all K steps in one launch (mk_decode_loop), the same
+        # per-step work; step latencies from the device clock at the step
+        # boundaries
+        reset()
+        if args.warmup:
+            model.decode_loop(args.warmup)
+        reset()
+        clk = torch.zeros(K + 1, dtype=torch.int64, device="cuda")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_start = time.perf_counter()
+        e0.record()
+        model.decode_loop(K, step_clock=clk)
+        e1.record()
+        torch.cuda.synchronize()
+        wall2 = time.perf_counter() - t_start
+        mean2 = e0.elapsed_time(e1) / K
+        hz = mk_lib.load().mk_wall_clock_hz(0)
+        step_ms2 = ((clk[1:] - clk[:-1]).double() * 1e3 / hz).cpu().tolist()
+        if per_launch is not None and not (torch.equal(model.tokens, ref_state[0])
+                                           and torch.equal(model.logits, ref_state[1])):
+            sys.exit("the decode loop's last token / logits differ from K single launches")
+        loop = {"value": round(K / wall2, 2), "ms_per_step": round(wall2 * 1e3 / K, 4),
+                "p50_step_ms": round(statistics.median(step_ms2), 4),
+                "p90_step_ms": round(sorted(step_ms2)[int(0.9 * (K - 1))], 4),
+                "kernel_ms_per_step": round(mean2, 4)}
     bits = model.ws.read_device_error()
     if bits:
         sys.exit(f"device error bits 0x{bits:x}")
+    head = loop if loop is not None else per_launch
     bytes_per_step = sum(step_bytes(16, [PROMPT + i], lm_head=True) for i in range(K)) / K
-    achieved = bytes_per_step / (mean_ms * 1e-3) / 1e9
+    achieved = bytes_per_step / (head["kernel_ms_per_step"] * 1e-3) / 1e9
+    if per_launch is not None:
+        a1 = bytes_per_step / (per_launch["kernel_ms_per_step"] * 1e-3) / 1e9
+        per_launch.update(achieved_gbs=round(a1, 1), frac=round(a1 / HBM_PEAK_GBS, 4))
 
     traffic, traffic_src = traffic_of("c3")
+    how = ("all K steps in one launch of mk_decode_kernel (mk_decode_loop: an on-device step barrier, each "
+           "step's argmax fed to the next)" if loop is not None else "one launch of mk_decode_kernel per step")
     result = {
         "metric": "bs=1 decode tok/s + p50 step latency, Llama-3.2-1B ctx1024; HBM GB/s",
-        "value": round(K / wall, 2),
+        "value": head["value"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / K, 4),
-        "p50_step_ms": round(statistics.median(step_ms), 4),
-        "p90_step_ms": round(sorted(step_ms)[int(0.9 * (K - 1))], 4),
+        "ms_per_step": head["ms_per_step"],
+        "p50_step_ms": head["p50_step_ms"],
+        "p90_step_ms": head["p90_step_ms"],
         "prefill_ms": round(prefill_ms, 3),
         "higher_is_better": True,
         "scaling": "weak",
@@ -292,10 +349,12 @@ def main():
         "data": "synthetic (random-init N(0,0.02) bf16 weights seed 0, uniform-random prompt ids seed 0)",
         "config": {"workload": "C3: Llama-3.2-1B decode, batch 1, 384-token prompt prefilled to a 1024-row "
                                f"KV cache, greedy steps at KV lengths {PROMPT}..{PROMPT + K - 1}",
-                   "batch": 1, "prompt": PROMPT, "max_context_length": S_MAX, "n_layers": 16},
+                   "batch": 1, "prompt": PROMPT, "max_context_length": S_MAX, "n_layers": 16,
+                   "steps_run_as": how},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "bytes_per_step": int(bytes_per_step), "kernel": "mk_decode_kernel"},
+        "per_launch": per_launch,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -484,6 +484,27 @@ class NeuronLlamaForCausalLMMK:
         return graph
 
     @torch.no_grad()
+    def decode_loop(self, n_steps: int, step_clock: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``n_steps`` greedy decode steps of a batch-1 model in ONE launch of the
+        persistent kernel (``mk_decode_loop``): each step feeds its argmax to
+        the next on the device, continuing from the model's current token and
+        position exactly as ``n_steps`` launches of ``launcher("decode")``
+        would (same tokens, caches, pos, and the last step's logits). Returns the
+        generated token ids (int32 [n_steps], on the device); ``step_clock``
+        (int64 [n_steps + 1]) receives the device wall clock at each step
+        boundary (``mk_wall_clock_hz`` ticks per second)."""
+        if self.batch_size != 1:
+            raise ValueError(f"the decode loop runs batch 1 (model batch {self.batch_size})")
+        p = int(self.pos[0])
+        if p + n_steps > self.s_max:
+            raise ValueError(f"{n_steps} steps from position {p} exceed max_context_length {self.s_max}")
+        out = torch.empty(n_steps, dtype=torch.int32, device=self.pos.device)
+        mk_lib.decode_loop(self.weights, self.ws, self.k_caches, self.v_caches, self.pos, self.tokens, n_steps,
+                           tokens_out=out, step_clock=step_clock, logits=self.logits, next_token=self.tokens,
+                           hidden_out=self.hidden_out, flags=mk_lib.MK_FLAG_ADVANCE)
+        return out
+
+    @torch.no_grad()
     def generate(self, input_ids, max_new_tokens: int, return_logits: bool = False,
                  sampling_params: Optional[torch.Tensor] = None, seed: int = 0):
         """Generation for the batch's sequences (prompts as in ``prefill``):
@@ -499,18 +520,22 @@ class NeuronLlamaForCausalLMMK:
             if int(p.numel()) + max_new_tokens - 1 > self.s_max:
                 raise ValueError(f"{int(p.numel())} + {max_new_tokens} tokens exceed max_context_length {self.s_max}")
         self.prefill(prompts)
-        dec = self.launcher("decode" if sampling_params is None else "decode_logits")
         sampling_params = self._sampling_rows(sampling_params)
         B = self.batch_size
-        out = torch.empty(max_new_tokens, B, dtype=torch.int32, device=self.pos.device)
         logits = [] if return_logits else None
-        for t in range(max_new_tokens):
-            dec.launch()
-            if sampling_params is not None:
-                mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
-            out[t].copy_(self.tokens)
-            if return_logits:
-                logits.append(self.logits.clone())
+        if B == 1 and sampling_params is None and not return_logits:
+            # greedy batch 1 with nothing to read between steps: one launch
+            out = self.decode_loop(max_new_tokens).view(max_new_tokens, 1)
+        else:
+            dec = self.launcher("decode" if sampling_params is None else "decode_logits")
+            out = torch.empty(max_new_tokens, B, dtype=torch.int32, device=self.pos.device)
+            for t in range(max_new_tokens):
+                dec.launch()
+                if sampling_params is not None:
+                    mk_lib.sample(self.logits, sampling_params, self.tokens, seed=seed, counter=self.pos)
+                out[t].copy_(self.tokens)
+                if return_logits:
+                    logits.append(self.logits.clone())
         torch.cuda.synchronize()
         bits = self.ws.read_device_error() | self.prefill_device_error()
         if bits:

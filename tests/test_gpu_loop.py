@@ -7,7 +7,8 @@ state (a 64-token prompt prefilled into a 256-row cache) the loop's tokens,
 its last step's logits and hidden state, every K/V cache byte and the advanced
 position equal those of 24 single launches bit for bit. A loop followed by
 single steps continues the exchange-set and argmax-key state (equal to the
-same number of single steps). The step clock is monotonic. Refusals: batch > 1
+same number of single steps). The step clock is monotonic. ``model.generate``
+(greedy, batch 1) runs the loop and returns the step-by-step tokens. Refusals: batch > 1
 workspace, hidden input, and positions past the cache (a device error, nothing
 written).
 """
@@ -133,3 +134,18 @@ def test_loop_refusals(model):
     # and the workspace is still good for a loop afterwards
     m.pos.fill_(10)
     loop(m, 3)
+
+
+def test_generate_runs_the_loop(model):
+    """Greedy batch-1 ``generate`` without logits runs the steps as one
+    ``mk_decode_loop`` launch; with logits it launches every step. Same tokens."""
+    from mk_weights import random_token_ids
+    m = model
+    ids = random_token_ids(50, seed=47)
+    stepwise, _ = m.generate(ids, 30, return_logits=True)
+    looped = m.generate(ids, 30)
+    say(f"[loop] generate: {looped[:8].tolist()}...")
+    assert torch.equal(looped, stepwise)
+    assert int(m.pos.item()) == 50 + 30 - 1
+    with pytest.raises(ValueError):
+        m.decode_loop(S)                 # past the cache: refused on the host
