@@ -301,10 +301,13 @@ def main():
             model.decode_loop(args.warmup)
         reset()
         clk = torch.zeros(K + 1, dtype=torch.int64, device="cuda")
+        toks_out = torch.empty(K, dtype=torch.int32, device="cuda")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
         t_start = time.perf_counter()
         e0.record()
-        model.decode_loop(K, step_clock=clk)
+        # (the step range was checked above: K <= S_MAX - PROMPT)
+        model.decode_loop(K, step_clock=clk, tokens_out=toks_out, check=False)
         e1.record()
         torch.cuda.synchronize()
         wall2 = time.perf_counter() - t_start

@@ -16,7 +16,9 @@ Mirrors the reference module ``llama_with_megakernel`` (selected by
   caches are updated in place at ``position_ids`` and returned as the same
   tensors;
 * ``generate(input_ids, max_new_tokens)`` — greedy decoding (the reference's
-  ``do_sample=False`` / ``top_k=1`` path, main.py:57, 291, 332).
+  ``do_sample=False`` / ``top_k=1`` path, main.py:57, 291, 332); at batch 1
+  without requested logits every step runs in one launch (``decode_loop``,
+  ``mk_decode_loop``).
 
 ``model_path`` is a local HF checkpoint directory (safetensors) or
 ``"random:<seed>"`` for the synthetic N(0, 0.02) weights used by the
@@ -484,21 +486,27 @@ class NeuronLlamaForCausalLMMK:
         return graph
 
     @torch.no_grad()
-    def decode_loop(self, n_steps: int, step_clock: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def decode_loop(self, n_steps: int, step_clock: Optional[torch.Tensor] = None,
+                    tokens_out: Optional[torch.Tensor] = None, check: bool = True) -> torch.Tensor:
         """``n_steps`` greedy decode steps of a batch-1 model in ONE launch of the
         persistent kernel (``mk_decode_loop``): each step feeds its argmax to
         the next on the device, continuing from the model's current token and
         position exactly as ``n_steps`` launches of ``launcher("decode")``
         would (same tokens, caches, pos, and the last step's logits). Returns the
-        generated token ids (int32 [n_steps], on the device); ``step_clock``
-        (int64 [n_steps + 1]) receives the device wall clock at each step
-        boundary (``mk_wall_clock_hz`` ticks per second)."""
+        generated token ids (int32 [n_steps], on the device; ``tokens_out`` if
+        given); ``step_clock`` (int64 [n_steps + 1]) receives the device wall
+        clock at each step boundary (``mk_wall_clock_hz`` ticks per second).
+        ``check`` reads the position back to refuse a range past the cache on
+        the host (a synchronisation); without it the device refuses such a
+        range (``MK_DEVERR_POS``, nothing written)."""
         if self.batch_size != 1:
             raise ValueError(f"the decode loop runs batch 1 (model batch {self.batch_size})")
-        p = int(self.pos[0])
-        if p + n_steps > self.s_max:
-            raise ValueError(f"{n_steps} steps from position {p} exceed max_context_length {self.s_max}")
-        out = torch.empty(n_steps, dtype=torch.int32, device=self.pos.device)
+        if check:
+            p = int(self.pos[0])
+            if p + n_steps > self.s_max:
+                raise ValueError(f"{n_steps} steps from position {p} exceed max_context_length {self.s_max}")
+        out = tokens_out if tokens_out is not None else torch.empty(n_steps, dtype=torch.int32,
+                                                                     device=self.pos.device)
         mk_lib.decode_loop(self.weights, self.ws, self.k_caches, self.v_caches, self.pos, self.tokens, n_steps,
                            tokens_out=out, step_clock=step_clock, logits=self.logits, next_token=self.tokens,
                            hidden_out=self.hidden_out, flags=mk_lib.MK_FLAG_ADVANCE)

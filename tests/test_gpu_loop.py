@@ -8,7 +8,8 @@ its last step's logits and hidden state, every K/V cache byte and the advanced
 position equal those of 24 single launches bit for bit. A loop followed by
 single steps continues the exchange-set and argmax-key state (equal to the
 same number of single steps). The step clock is monotonic. ``model.generate``
-(greedy, batch 1) runs the loop and returns the step-by-step tokens. Refusals: batch > 1
+(greedy, batch 1) runs the loop and returns the step-by-step tokens; a HIP graph
+of a loop replays it exactly. Refusals: batch > 1
 workspace, hidden input, and positions past the cache (a device error, nothing
 written).
 """
@@ -149,3 +150,41 @@ def test_generate_runs_the_loop(model):
     assert int(m.pos.item()) == 50 + 30 - 1
     with pytest.raises(ValueError):
         m.decode_loop(S)                 # past the cache: refused on the host
+
+
+def test_loop_in_a_graph(model):
+    """``mk_decode_loop`` is capturable (no allocation, no memset): a HIP graph of
+    one 6-step loop, replayed three times from the same state with eager steps
+    and synchronisations between the replays, equals the eager loop each time."""
+    import mk_lib
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(30, seed=51))
+    st = snapshot(m)
+    ref = loop(m, 6)
+    ref_kv, ref_logits = m.kv.clone(), m.logits.clone()
+    restore(m, st)
+    out = torch.full((6,), -5, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        mk_lib.decode_loop(m.weights, m.ws, m.k_caches, m.v_caches, m.pos, m.tokens, 6, tokens_out=out,
+                           logits=m.logits, next_token=m.tokens, hidden_out=m.hidden_out,
+                           flags=mk_lib.MK_FLAG_ADVANCE)
+    m.ws.register_graph(graph)
+    for rep in range(3):
+        restore(m, st)
+        singles(m, 2)                    # eager steps between the replays
+        restore(m, st)
+        out.fill_(-5)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert m.ws.read_device_error() == 0
+        say(f"[loop] graph replay {rep}: {out[:6].tolist()}")
+        assert torch.equal(out.cpu(), ref), rep
+        assert int(m.pos.item()) == int(st["pos"].item()) + 6
+        assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16)), rep
+        assert torch.equal(m.logits.view(torch.int32), ref_logits.view(torch.int32)), rep
+    del graph
