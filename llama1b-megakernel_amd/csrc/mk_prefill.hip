@@ -80,6 +80,10 @@ struct GemmStage {
 struct GemmLds {
   GemmStage st[GEMM_NS];
 };
+// The epilogue's side input in LDS: PF_TM rows of 128 bf16, padded to 136
+// (a 272-byte row stride spreads the rows of one read over the banks).
+constexpr int SIDE_LD = 136;
+static_assert(PF_TM * SIDE_LD * 2 <= (int)sizeof(GemmLds), "side input over the operand stages");
 
 template <int EPI>
 __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
@@ -110,6 +114,29 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&L.st[stg].b[2 * wave + u][0], 16, bo, 0, 0, 0);
     }
   };
+  // The epilogue's side input, 128 rows of 256 bytes: the RoPE rows of the
+  // tile's tokens (EPI_QKV) or the residual tile (EPI_RES). Two threads per
+  // row load it with 16-byte loads before the first operand copies (so they
+  // are the oldest loads in flight and land first); it goes to LDS after the
+  // k-loop, so the epilogue reads LDS instead of waiting on a 2-byte global
+  // load per element. Rows past the tokens read zero.
+  constexpr bool SIDE = EPI == EPI_QKV || EPI == EPI_RES;
+  const int srow = threadIdx.x >> 1, shalf = threadIdx.x & 1;
+  u32x4 side[SIDE ? 8 : 1];
+  if constexpr (SIDE) {
+    const int m = tm * PF_TM + srow;
+    rsrc_t rs;
+    uint32_t off = OOB;
+    if constexpr (EPI == EPI_RES) {
+      rs = make_rsrc(g.res, (size_t)g.M * g.N * 2);
+      if (m < g.M) off = (uint32_t)(((size_t)m * g.N + (size_t)tn * PF_TN) * 2) + (uint32_t)shalf * 128u;
+    } else {
+      rs = make_rsrc(g.rope, (size_t)g.s_max * (4 * HD));
+      if (m < g.M) off = (uint32_t)((size_t)(g.p0 + m) * (4 * HD)) + (uint32_t)shalf * 128u;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) side[k] = ld16(rs, off == OOB ? OOB : off + 16u * (uint32_t)k);
+  }
   // wave (wm, wn) computes rows 64*wm .. +63 and columns 64*wn .. +63 of the tile
   const int wm = wave & 1, wn = wave >> 1;
   f32x4 acc[4][4];
@@ -123,8 +150,9 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
 #pragma unroll
     for (int s = 0; s < GEMM_NS; ++s) {
       // this wave's copies of stage s have landed (the GEMM_NS - 2 later
-      // stages' 4 copies each may be in flight), and, after the barrier, every
-      // wave's; every wave has also finished reading the stage refilled next
+      // stages' 4 copies each may be in flight; the side loads, issued
+      // first, have landed too), and, after the barrier, every wave's; every
+      // wave has also finished reading the stage refilled next
       static_assert(GEMM_NS == 4, "the wait below counts 2 later stages of 4 copies");
       asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
       issue(ks + s + GEMM_NS - 1, (s + GEMM_NS - 1) % GEMM_NS);
@@ -141,6 +169,16 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
     }
   }
   const int am = tm * 8 + 4 * wm, bn = tn * 8 + 4 * wn;   // the wave's first A / B tile
+  // the side input into LDS, over the operand stages: every wave's operand
+  // reads and copies (the trailing ones write zeros into the stages) are done
+  const uint16_t* side_lds = reinterpret_cast<const uint16_t*>(&L);   // [PF_TM][SIDE_LD]
+  if constexpr (SIDE) {
+    __syncthreads();
+    u32x4* dst = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(&L) + srow * SIDE_LD + shalf * 64);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[k] = side[k];
+    __syncthreads();
+  }
 
   // epilogue: acc[i][j][r] is (row 16*(am+i) + 4*(lane/16) + r, column 16*(bn+j) + lane%16)
 #pragma unroll
@@ -156,8 +194,8 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
           if (m < g.M) g.part[((size_t)blockIdx.y * g.M + m) * g.N + n] = v;
         } else if constexpr (EPI == EPI_RES) {
           if (m < g.M) {
-            const size_t o = (size_t)m * g.N + n;
-            g.out[o] = (uint16_t)f2bf(bf2f(g.res[o]) + rbf(v));
+            const uint16_t r0 = side_lds[(m - tm * PF_TM) * SIDE_LD + (n - tn * PF_TN)];
+            g.out[(size_t)m * g.N + n] = (uint16_t)f2bf(bf2f(r0) + rbf(v));
           }
         } else if constexpr (EPI == EPI_SWIGLU) {
           // rows (gate_i, up_i) interleaved: lanes 2k (gate) and 2k+1 (up)
@@ -171,7 +209,7 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
           if (m < g.M) {
             const int pair = n >> 1, e = n & 1, pos = g.p0 + m;
             const int hp = pair & 31;                      // d = hp + 32e
-            const uint16_t* rrow = g.rope + (size_t)pos * (2 * HD);
+            const uint16_t* rrow = side_lds + (m - tm * PF_TM) * SIDE_LD;   // row pos of the RoPE table
             float o = x;
             if (pair < Q_PAIRS + K_PAIRS) {
               const float a = e ? y : x, b = e ? x : y;    // the pair (x[d], x[d+32])
