@@ -233,33 +233,53 @@ __global__ void __launch_bounds__(NT) pf_gemm(GemmArgs g) {
   }
 }
 
-// The split-K tail of the O and down projections (N = 2048), one wave per
-// token row t: v = the sum of the `splits` fp32 partials in order, out =
-// bf16(res + bf16(v)) (row-major), and, if xn is given, the next RMSNorm of
-// out into xn (A-tile order), as pf_norm computes it.
-__global__ void __launch_bounds__(NT) pf_reduce_norm(const float* part, int splits, const uint16_t* res,
-                                                     uint16_t* out, uint16_t* xn, int T) {
-  const int t = blockIdx.x * NWAVE + wave_id(), lane = lane_id();
+// The split-K tail of the O and down projections (N = 2048), one 64-thread
+// workgroup per token row t (the rows spread over every CU): v = the sum of
+// the SPLITS fp32 partials in split order, out = bf16(res + bf16(v))
+// (row-major), and, if xn is given, the next RMSNorm of out into xn (A-tile
+// order), as pf_norm computes it. Every partial of a group of chunks is
+// loaded before the first sum, so the loads overlap instead of waiting one
+// split at a time.
+template <int SPLITS>
+__global__ void __launch_bounds__(64) pf_reduce_norm(const float* part, const uint16_t* res, uint16_t* out,
+                                                     uint16_t* xn, int T) {
+  const int t = blockIdx.x, lane = lane_id();
   if (t >= T) return;
+  constexpr int CH = SPLITS <= 4 ? 4 : (SPLITS <= 8 ? 2 : 1);   // 512-column chunks loaded at once
   u32x4 xs[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = i * 512 + lane * 8;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < splits; ++s) {
-      const float4* pp = reinterpret_cast<const float4*>(part + ((size_t)s * T + t) * H + c);
-      const float4 p0 = pp[0], p1 = pp[1];
-      v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
-      v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
-    }
-    const u32x4 rv = *reinterpret_cast<const u32x4*>(res + (size_t)t * H + c);
-    const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
-    uint32_t o[4];
+  for (int i0 = 0; i0 < 4; i0 += CH) {
+    float4 pv[CH][SPLITS][2];
+    u32x4 rv[CH];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = f2bf(bf_lo(rw[e]) + rbf(v[2 * e])) | (f2bf(bf_hi(rw[e]) + rbf(v[2 * e + 1])) << 16);
-    xs[i] = u32x4{o[0], o[1], o[2], o[3]};
-    *reinterpret_cast<u32x4*>(out + (size_t)t * H + c) = xs[i];
+    for (int ci = 0; ci < CH; ++ci) {
+      const int c = (i0 + ci) * 512 + lane * 8;
+#pragma unroll
+      for (int sp = 0; sp < SPLITS; ++sp) {
+        const float4* pp = reinterpret_cast<const float4*>(part + ((size_t)sp * T + t) * H + c);
+        pv[ci][sp][0] = pp[0];
+        pv[ci][sp][1] = pp[1];
+      }
+      rv[ci] = *reinterpret_cast<const u32x4*>(res + (size_t)t * H + c);
+    }
+#pragma unroll
+    for (int ci = 0; ci < CH; ++ci) {
+      float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < SPLITS; ++sp) {
+        const float4 p0 = pv[ci][sp][0], p1 = pv[ci][sp][1];
+        v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
+        v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
+      }
+      const uint32_t rw[4] = {rv[ci].x, rv[ci].y, rv[ci].z, rv[ci].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = f2bf(bf_lo(rw[e]) + rbf(v[2 * e])) | (f2bf(bf_hi(rw[e]) + rbf(v[2 * e + 1])) << 16);
+      const int i = i0 + ci;
+      xs[i] = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4*>(out + (size_t)t * H + i * 512 + lane * 8) = xs[i];
+    }
   }
   if (!xn) return;
   rmsnorm2048(xs, nullptr);
@@ -493,8 +513,13 @@ hipError_t prefill_launch(const mk_weights* w, const mk_prefill_args* a, int cap
       g.splits = sp;
       g.part = part;
       hipLaunchKernelGGL(pf_gemm<EPI_PART>, dim3(mt * (H / PF_TN), sp), dim3(NT), 0, st, g);
-      hipLaunchKernelGGL(pf_reduce_norm, tg, dim3(NT), 0, st, (const float*)part, sp, res, out,
-                         norm ? xn : (uint16_t*)nullptr, T);
+      uint16_t* xn_out = norm ? xn : nullptr;
+      switch (sp) {   // res_splits gives 2, 4, 8 or 16
+        case 2: hipLaunchKernelGGL(pf_reduce_norm<2>, dim3(T), dim3(64), 0, st, (const float*)part, res, out, xn_out, T); break;
+        case 4: hipLaunchKernelGGL(pf_reduce_norm<4>, dim3(T), dim3(64), 0, st, (const float*)part, res, out, xn_out, T); break;
+        case 8: hipLaunchKernelGGL(pf_reduce_norm<8>, dim3(T), dim3(64), 0, st, (const float*)part, res, out, xn_out, T); break;
+        default: hipLaunchKernelGGL(pf_reduce_norm<16>, dim3(T), dim3(64), 0, st, (const float*)part, res, out, xn_out, T); break;
+      }
     }
   };
   // Every chunk starts again from the embeddings of its own tokens; the rows
