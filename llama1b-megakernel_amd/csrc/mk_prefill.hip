@@ -29,7 +29,8 @@
 // of their use; each wave reads its 4 A and 4 B operands of a k-step from LDS
 // (a block per instruction, conflict-free) and runs 16 MFMAs. The O and down
 // projections of short prompts (few row tiles) split K across workgroups into
-// fp32 partials that pf_reduce_norm sums in a fixed order.
+// fp32 partials that pf_reduce_norm sums in a fixed order; so does the QKV
+// projection, whose tail (pf_qkv_finish) then applies RoPE and scatters.
 //
 // Attention: per (kv head, block of 16 tokens) one workgroup; S^T = K Q^T on
 // the matrix cores (keys on M, the 16 tokens x 4 q heads on N), an online
@@ -287,6 +288,56 @@ __global__ void __launch_bounds__(64) pf_reduce_norm(const float* part, const ui
   for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(xn + a_tile_off(t, i * 512 + lane * 8, H / 32)) = xs[i];
 }
 
+// The split-K tail of the QKV projection of short prompts (N = 3072), one
+// 64-thread workgroup per token row t: each RoPE pair p (columns 2p and
+// 2p + 1: dims d and d + 32 of a head) summed over the SPLITS fp32 partials
+// in split order and rounded to bf16, RoPE on the q and k pairs as the QKV
+// GEMM's epilogue does it, q to the q buffer, k and v to the caches at row
+// p0 + t.
+template <int SPLITS>
+__global__ void __launch_bounds__(64) pf_qkv_finish(const float* part, const uint16_t* rope, uint16_t* q,
+                                                    uint16_t* kc, uint16_t* vc, int T, int p0, int s_max) {
+  const int t = blockIdx.x, lane = lane_id();
+  if (t >= T) return;
+  const int pos = p0 + t;
+  const uint16_t* rrow = rope + (size_t)pos * (2 * HD);
+  constexpr int PER = 4;   // pairs per thread whose partials are loaded at once
+  static_assert(QKV_PAIRS % (64 * PER) == 0, "pair groups");
+#pragma unroll 1
+  for (int p0g = 0; p0g < QKV_PAIRS; p0g += 64 * PER) {
+    float2 pv[PER][SPLITS];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+#pragma unroll
+      for (int sp = 0; sp < SPLITS; ++sp)
+        pv[j][sp] = *reinterpret_cast<const float2*>(part + ((size_t)sp * T + t) * QKV_ROWS + 2 * (p0g + j * 64 + lane));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int pr = p0g + j * 64 + lane, hp = pr & 31;
+      float va = 0.f, vb = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < SPLITS; ++sp) {
+        va += pv[j][sp].x;
+        vb += pv[j][sp].y;
+      }
+      const float a = rbf(va), b = rbf(vb);   // (x[d], x[d + 32]) with d = hp
+      float o0 = a, o1 = b;
+      if (pr < Q_PAIRS + K_PAIRS) {
+        const float c0 = bf2f(rrow[hp]), s0 = bf2f(rrow[HD + hp]);
+        const float c1 = bf2f(rrow[hp + 32]), s1 = bf2f(rrow[HD + hp + 32]);
+        o0 = rbf(rbf(a * c0) + rbf(-b * s0));
+        o1 = rbf(rbf(b * c1) + rbf(a * s1));
+      }
+      uint16_t* dst;
+      if (pr < Q_PAIRS) dst = q + (size_t)t * H + (pr >> 5) * HD;
+      else if (pr < Q_PAIRS + K_PAIRS) dst = kc + ((size_t)((pr - Q_PAIRS) >> 5) * s_max + pos) * HD;
+      else dst = vc + ((size_t)((pr - Q_PAIRS - K_PAIRS) >> 5) * s_max + pos) * HD;
+      dst[hp] = (uint16_t)f2bf(o0);
+      dst[hp + 32] = (uint16_t)f2bf(o1);
+    }
+  }
+}
+
 // xn (A-tile order [T16][2048]) = bf16(x * rsqrt(mean(x^2) + eps)) per token
 // row, one wave per token; with `tokens`, x is the embedding row of the token
 // and is also copied to x_out (row-major) as the first residual.
@@ -462,6 +513,16 @@ int res_splits(int mt, int kb) {
   return s;
 }
 
+// K splits of the QKV projection (N = 3072, 24 column tiles) over mt row
+// tiles: up to one round of the 256-CU grid, the partials within PART_BYTES.
+int qkv_splits(int mt) {
+  int s = 1;
+  while (mt * (QKV_ROWS / PF_TN) * s * 2 <= 256 && ((H / 32) / (s * 2)) % GEMM_NS == 0 &&
+         (size_t)s * 2 * mt * PF_TM * QKV_ROWS * 4 <= PART_BYTES)
+    s *= 2;
+  return s;
+}
+
 }  // namespace
 
 namespace mk {
@@ -551,7 +612,21 @@ hipError_t prefill_launch(const mk_weights* w, const mk_prefill_args* a, int cap
       g.out = q;
       g.kc = kc;
       g.vc = vc;
-      hipLaunchKernelGGL(pf_gemm<EPI_QKV>, dim3(mt * (QKV_ROWS / PF_TN)), dim3(NT), 0, st, g);
+      const int qs = qkv_splits(mt);
+      if (qs == 1) {
+        hipLaunchKernelGGL(pf_gemm<EPI_QKV>, dim3(mt * (QKV_ROWS / PF_TN)), dim3(NT), 0, st, g);
+      } else {   // short prompts: split over K, RoPE and the scatter in the tail
+        g.splits = qs;
+        g.part = part;
+        hipLaunchKernelGGL(pf_gemm<EPI_PART>, dim3(mt * (QKV_ROWS / PF_TN), qs), dim3(NT), 0, st, g);
+        const uint16_t* rope = static_cast<const uint16_t*>(w->rope);
+        switch (qs) {   // qkv_splits gives 2, 4 or 8
+          case 2: hipLaunchKernelGGL(pf_qkv_finish<2>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+          case 4: hipLaunchKernelGGL(pf_qkv_finish<4>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+          default: hipLaunchKernelGGL(pf_qkv_finish<8>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+        }
+        g.splits = 1;
+      }
       if (tail) break;   // the last layer's K/V rows are all the caller needs
       AttnArgs aa;
       aa.q = q;
