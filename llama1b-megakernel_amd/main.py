@@ -172,6 +172,9 @@ def parse_args(argv=None):
                     help="accepted: the residual add is always fused")
     # this build's benchmark mode
     ap.add_argument("--graph", action="store_true", help="benchmark: replay the decode steps as one HIP graph")
+    ap.add_argument("--decode-loop", action="store_true",
+                    help="benchmark: greedy batch-1 token generation as one mk_decode_loop launch (per-step latencies "
+                         "from the device clock at the step boundaries)")
     ap.add_argument("--num-runs", type=int, default=5)
     ap.add_argument("--report-path", default=BENCHMARK_REPORT_FILENAME)
     args = ap.parse_args(argv)
@@ -475,13 +478,23 @@ def benchmark_sampling(args):
     e2e, context encoding (prefill) and per-step token generation latencies
     over num_runs runs after one warm-up run. With --graph the token-generation
     steps of a run replay one captured HIP graph (the per-step latency is then
-    the run's generation time / steps)."""
+    the run's generation time / steps); with --decode-loop (greedy, batch 1)
+    they run as one mk_decode_loop launch and the per-step latencies are the
+    device clock's intervals between step boundaries."""
     import mk_lib
     prompts = encode_prompts(args, args_tokenizer(args))
     B = len(prompts)
+    loop = getattr(args, "decode_loop", False)
+    greedy = not args.do_sample or args.top_k == 1
+    if loop and (not greedy or B != 1 or args.graph):
+        raise SystemExit("--decode-loop runs greedy batch-1 generation (no sampling, one prompt, no --graph)")
     model = prepare_inference(args, B)
     n_new = max_new_tokens(args, prompts)
     sp = sampling_params(args, B)
+    if loop:
+        clk = torch.zeros(n_new + 1, dtype=torch.int64, device=model.pos.device)
+        toks_out = torch.empty(n_new, dtype=torch.int32, device=model.pos.device)
+        hz = mk_lib.load().mk_wall_clock_hz(model.pos.device.index or 0)
     dec = model.launcher("decode" if sp is None else "decode_logits")
     graph = model.decode_graph(n_new, sampling_params=sp, seed=args.seed) if args.graph else None
     e2e, cte, tkg = [], [], []
@@ -492,7 +505,9 @@ def benchmark_sampling(args):
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_new + 1)]
-        if graph is not None:
+        if loop:
+            model.decode_loop(n_new, step_clock=clk, tokens_out=toks_out, check=False)
+        elif graph is not None:
             ev[0].record()
             graph.replay()
             ev[n_new].record()
@@ -509,7 +524,9 @@ def benchmark_sampling(args):
             continue            # warm-up run
         e2e.append((t2 - t0) * 1e3)
         cte.append((t1 - t0) * 1e3)
-        if graph is not None:
+        if loop:
+            tkg += ((clk[1:] - clk[:-1]).double() * 1e3 / hz).cpu().tolist()
+        elif graph is not None:
             tkg += [ev[0].elapsed_time(ev[n_new]) / n_new] * n_new
         else:
             tkg += [ev[i].elapsed_time(ev[i + 1]) for i in range(n_new)]
@@ -521,7 +538,8 @@ def benchmark_sampling(args):
               "context_encoding_model": generate_report(cte, n_prompt),
               "token_generation_model": generate_report(tkg, B),
               "config": {"batch": B, "prompt_lengths": [int(p.numel()) for p in prompts], "max_new_tokens": n_new,
-                         "graph": bool(args.graph), "num_runs": args.num_runs, "model_path": args.model_path}}
+                         "graph": bool(args.graph), "decode_loop": bool(loop), "num_runs": args.num_runs,
+                         "model_path": args.model_path}}
     print(json.dumps(report, indent=4))
     Path(args.report_path).write_text(json.dumps(report))
     return report

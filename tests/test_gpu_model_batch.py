@@ -15,7 +15,7 @@
 * A safetensors checkpoint written from the seed-0 weights and read back
   through ``load_hf_checkpoint`` (the model_path of a real checkpoint) gives
   logits bit-identical to the ``random:0`` weights (2-layer model, full vocab).
-* ``main.py --mode benchmark`` with and without ``--graph`` writes a report
+* ``main.py --mode benchmark`` plain, with ``--graph`` and with ``--decode-loop`` writes a report
   with the e2e / context-encoding / token-generation sections (main.py:178-271).
 """
 
@@ -132,13 +132,14 @@ def test_checkpoint_directory_matches_random_weights(tmp_path):
 
 
 @pytest.mark.timeout(300)
-@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("graph", [False, True, "loop"])
 def test_main_benchmark_report(tmp_path, graph):
     need_gpu()
     import main
     path = tmp_path / "benchmark_report.json"
+    extra = {False: [], True: ["--graph"], "loop": ["--decode-loop"]}[graph]
     argv = ["--mode", "benchmark", "--enable-nki", "--prompt-len", "64", "--max-new-tokens", "32",
-            "--seq-len", "128", "--num-runs", "2", "--report-path", str(path)] + (["--graph"] if graph else [])
+            "--seq-len", "128", "--num-runs", "2", "--report-path", str(path)] + extra
     assert main.main(argv) == 0
     rep = json.loads(path.read_text())
     for key in ("e2e_model", "context_encoding_model", "token_generation_model"):

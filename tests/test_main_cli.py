@@ -195,3 +195,13 @@ def test_compiled_model_path_manifest(tmp_path, small):
     f.write_text(json.dumps(d))
     with pytest.raises(ValueError, match="libmk_sha256"):
         m.check_manifest(str(tmp_path / "c"))
+
+
+@pytest.mark.parametrize("extra", [["--do-sample", "True", "--top-k", "50"], ["--graph"]])
+def test_benchmark_decode_loop_needs_greedy_batch1(extra):
+    """``--decode-loop`` (one mk_decode_loop launch for the token generation) is
+    greedy batch 1 only; sampling or a graph is refused before any GPU work."""
+    import main
+    with pytest.raises(SystemExit, match="--decode-loop"):
+        main.main(["--mode", "benchmark", "--enable-nki", "--decode-loop", "--prompt-len", "8",
+                   "--max-new-tokens", "4", "--seq-len", "64"] + extra)
