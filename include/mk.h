@@ -301,7 +301,8 @@ int mk_decode_step(const mk_weights *w, const mk_step_args *a);
  *     to workgroup 0 (entry n + 1, n < n_steps - 1), and when the launch
  *     ended (entry n_steps): entry differences are per-step latencies.
  *   MK_ERR_UNSUPPORTED for batch > 1, hidden_in, MK_FLAG_PREFILL or a batched
- *   workspace. Asynchronous on the stream; allocates nothing.
+ *   workspace; MK_ERR_NULL without w->norm_final (every step runs the lm_head).
+ *   Asynchronous on the stream; allocates nothing.
  */
 int mk_decode_loop(const mk_weights *w, const mk_step_args *a, int32_t n_steps, int32_t *tokens_out,
                    uint64_t *step_clock);

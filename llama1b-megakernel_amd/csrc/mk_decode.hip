@@ -879,9 +879,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   if (p.n_steps > 1) {   // a loop: both keys and the step counters start the next launch at zero
     *key_ptr(p.n_steps) = 0ull;
     for (int j = 0; j < STEP_LINES; ++j) p.step_cnt[(size_t)j * (STEP_LINE / 4)] = 0u;
-    if (p.step_clock) p.step_clock[p.n_steps] = wall_clock64();
-    if (pos_ok && p.tokens_out) p.tokens_out[p.n_steps - 1] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   }
+  if (p.step_clock) p.step_clock[p.n_steps] = wall_clock64();
+  if (pos_ok && p.tokens_out) p.tokens_out[p.n_steps - 1] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   if (p.noalloc) {
     // In the static scratch the step's error bits are cleared so the next
     // step's waits do not bail out; a faulted step reports next_token = -1
@@ -1131,7 +1131,8 @@ int check_step_args(const mk_weights* w, const mk_step_args* a) {
 // Enqueue mk_decode_kernel (batch 1) with control block `ctrl` and exchange sets `xch`.
 int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& di, uint8_t* ctrl, uint8_t* xch,
                   bool noalloc, int n_steps = 1, int32_t* tokens_out = nullptr, uint64_t* step_clock = nullptr) {
-  const bool do_lm = a->logits != nullptr || a->next_token != nullptr || n_steps > 1;
+  // (a loop, or a caller of it that asks for the tokens, needs every step's argmax)
+  const bool do_lm = a->logits != nullptr || a->next_token != nullptr || n_steps > 1 || tokens_out != nullptr;
   KParams kp;
   memset(&kp, 0, sizeof(kp));
   kp.w_qkv = static_cast<const uint16_t*>(w->w_qkv);
@@ -1385,6 +1386,7 @@ int mk_decode_loop(const mk_weights* w, const mk_step_args* a, int32_t n_steps, 
   if (a->batch != 1) return fail(MK_ERR_UNSUPPORTED, "the decode loop runs batch 1 (batch %d)", a->batch);
   if (!a->tokens || a->hidden_in)
     return fail(MK_ERR_UNSUPPORTED, "the decode loop takes token input (each step's token is the last one's argmax)");
+  if (!w->norm_final) return fail(MK_ERR_NULL, "norm_final is NULL (every step of the loop runs the lm_head)");
   if (a->flags & MK_FLAG_PREFILL) return fail(MK_ERR_UNSUPPORTED, "MK_FLAG_PREFILL is not a decode loop");
   if ((tokens_out && !aligned16(tokens_out)) || (step_clock && !aligned16(step_clock)))
     return fail(MK_ERR_ALIGN, "tokens_out / step_clock not 16-byte aligned");

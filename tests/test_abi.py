@@ -132,6 +132,24 @@ def test_noalloc_step_argument_checks(lib):
     assert lib.mk_decode_step_noalloc(ctypes.byref(w), ctypes.byref(a)) == -1
 
 
+def test_decode_loop_argument_checks(lib):
+    """mk_decode_loop: n_steps in [1, 2^20], batch 1, token input, the final
+    norm's weights (every step runs the lm_head), aligned outputs; all checked
+    before any HIP call."""
+    w = _weights()
+    a, keep = _args()
+    assert lib.mk_decode_loop(ctypes.byref(w), ctypes.byref(a), 0, None, None) == -2
+    assert lib.mk_decode_loop(ctypes.byref(w), ctypes.byref(a), (1 << 20) + 1, None, None) == -2
+    a, keep = _args(batch=2)
+    assert lib.mk_decode_loop(ctypes.byref(w), ctypes.byref(a), 4, None, None) == -4
+    a, keep = _args(next_token=None)
+    assert lib.mk_decode_loop(ctypes.byref(_weights(norm_final=None)), ctypes.byref(a), 4, None, None) == -1
+    assert b"norm_final" in lib.mk_last_error()
+    a, keep = _args()
+    assert lib.mk_decode_loop(ctypes.byref(w), ctypes.byref(a), 4, 0x9001, None) == -7
+    assert lib.mk_decode_loop(ctypes.byref(w), ctypes.byref(a), 4, None, 0x9008) == -7
+
+
 def _pf_args(**over):
     import mk_lib
     kc = (c_void_p * 16)(*([0x1000] * 16))

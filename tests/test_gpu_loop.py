@@ -188,3 +188,22 @@ def test_loop_in_a_graph(model):
         assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16)), rep
         assert torch.equal(m.logits.view(torch.int32), ref_logits.view(torch.int32)), rep
     del graph
+
+
+def test_one_step_loop(model):
+    """A loop of one step is one single step: it writes its token and both
+    step-clock entries, and equals a single launch bit for bit."""
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(20, seed=53))
+    st = snapshot(m)
+    ref = singles(m, 1)
+    ref_logits, ref_kv = m.logits.clone(), m.kv.clone()
+    restore(m, st)
+    clock = torch.zeros(2, dtype=torch.int64, device="cuda")
+    got = loop(m, 1, clock)
+    assert torch.equal(got, ref)
+    assert torch.equal(m.logits.view(torch.int32), ref_logits.view(torch.int32))
+    assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
+    c = clock.cpu()
+    assert int(c[1]) > int(c[0]) > 0, c.tolist()
