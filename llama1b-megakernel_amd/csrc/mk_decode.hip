@@ -341,6 +341,7 @@ struct Ctx {
   bool has_o;            // the workgroup has O rows
   Span gu_pairs;         // this wave's gate/up pairs
   Span d_rows;           // this wave's down-projection rows
+  bool loop;             // a decode loop (the kernel's LOOP instantiation): cache rows by device-scope stores
 
   __device__ __forceinline__ uint16_t* xb(int li, size_t off) const {
     return reinterpret_cast<uint16_t*>(set + (size_t)li * X_LAYER + off);
@@ -428,7 +429,7 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, R
       // the cache row: read by later launches (a plain store), or, in a decode
       // loop, by the next step of this launch on any XCD (a device-scope store)
       uint16_t* crow = (is_k ? kcl : vcl) + ((size_t)kh * p.s_max + c.pos) * HD + d;
-      if (p.n_steps > 1) {
+      if (c.loop) {
         st_dev(crow, o.x);
         st_dev(crow + 32, o.y);
       } else {
@@ -481,18 +482,23 @@ __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
 // GFIX: the grid size when it is known at compile time (the work splits then
 // divide by a constant: multiply and shift instead of a ~20-instruction
 // division each, ~1.8 us of the prologue at one wave per SIMD); 0: gridDim.x.
-template <int GFIX>
+// LOOP: the decode loop's instantiation (p.n_steps steps, the step barrier,
+// tokens_out / step_clock); without it the kernel is one step and carries
+// none of that code.
+template <int GFIX, bool LOOP>
 __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   __shared__ Lds L;
 
   Ctx c;
   c.p = &p;
+  c.loop = LOOP;
+  const int n_steps = LOOP ? p.n_steps : 1;
   uint32_t* ctrl = reinterpret_cast<uint32_t*>(p.ws);
   c.s.err = ctrl + C_ERR;
   c.s.timeout = p.timeout_ticks;
   c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
   trace_mark(c.s, 0);
-  if (p.step_clock && blockIdx.x == 0 && threadIdx.x == 0) p.step_clock[0] = wall_clock64();
+  if (LOOP && p.step_clock && blockIdx.x == 0 && threadIdx.x == 0) p.step_clock[0] = wall_clock64();
   c.G = GFIX ? GFIX : (int)gridDim.x;
   c.w = blockIdx.x;
   // The control words, the position and the token first; then the first
@@ -518,7 +524,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     for (int i = lo + threadIdx.x; i < hi; i += NT) other[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   };
   const int pos0 = c.pos;   // a loop's step n runs at position pos0 + n
-  const bool pos_ok = c.pos >= 0 && c.pos + p.n_steps <= p.s_max && c.pos + p.n_steps <= p.rope_rows;
+  const bool pos_ok = c.pos >= 0 && c.pos + n_steps <= p.s_max && c.pos + n_steps <= p.rope_rows;
   if (!p.do_lm || !pos_ok) refill(0);   // (the lm_head phase runs only with a valid position)
   if (!pos_ok && blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -559,8 +565,8 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     c.x_in = p.embed + (size_t)t * H;
   };
 
-  if (pos_ok) for (int n = 0; n < p.n_steps; ++n) {
-    const bool last_step = n + 1 == p.n_steps;
+  if (pos_ok) for (int n = 0; n < n_steps; ++n) {
+    const bool last_step = n + 1 == n_steps;
     if (n > 0) {
       c.pos = pos0 + n;
       c.n_rows = c.pos + 1;
@@ -600,7 +606,9 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       auto gidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_QKV>(L.spare); };
       auto oidle = [&]() { gpf.issue_fixed<GU_LDS_STEP_O>(L.spare); };
       if (li > 0) qkv_ring(c, li, qs);
-      if (li == 0 && n > 0) step_entry(n, gidle);
+      if constexpr (LOOP) {
+        if (li == 0 && n > 0) step_entry(n, gidle);
+      }
       phase_qkv(c, li, L, gidle, qs, [&]() {
         if (li == 0 && threadIdx.x < HD) reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] = rope_v;
       });
@@ -869,19 +877,21 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   __syncthreads();
   if (!L.last || threadIdx.x != 0) return;
   ctrl[C_EXIT] = 0u;
-  ctrl[C_EPOCH] = epoch + (pos_ok ? (uint32_t)p.n_steps : 1u);
+  ctrl[C_EPOCH] = epoch + (pos_ok ? (uint32_t)n_steps : 1u);
   unsigned long long key = 0ull;
   if (pos_ok && p.do_lm) {
-    unsigned long long* kp = key_ptr(p.n_steps - 1);
+    unsigned long long* kp = key_ptr(n_steps - 1);
     key = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *kp = 0ull;
   }
-  if (p.n_steps > 1) {   // a loop: both keys and the step counters start the next launch at zero
-    *key_ptr(p.n_steps) = 0ull;
-    for (int j = 0; j < STEP_LINES; ++j) p.step_cnt[(size_t)j * (STEP_LINE / 4)] = 0u;
+  if constexpr (LOOP) {
+    if (n_steps > 1) {   // both keys and the step counters start the next launch at zero
+      *key_ptr(n_steps) = 0ull;
+      for (int j = 0; j < STEP_LINES; ++j) p.step_cnt[(size_t)j * (STEP_LINE / 4)] = 0u;
+    }
+    if (p.step_clock) p.step_clock[n_steps] = wall_clock64();
+    if (pos_ok && p.tokens_out) p.tokens_out[n_steps - 1] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   }
-  if (p.step_clock) p.step_clock[p.n_steps] = wall_clock64();
-  if (pos_ok && p.tokens_out) p.tokens_out[p.n_steps - 1] = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
   if (p.noalloc) {
     // In the static scratch the step's error bits are cleared so the next
     // step's waits do not bail out; a faulted step reports next_token = -1
@@ -932,10 +942,14 @@ DeviceInfo g_dev[64];
 std::mutex g_dev_mu;
 
 // The batch-1 kernel for a grid of `grid` workgroups (one per CU): MI355X's 256
-// CUs get the instantiation with the grid size fixed at compile time.
-const void* decode_kernel_for(int grid) {
-  return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256>)
-                     : reinterpret_cast<const void*>(mk_decode_kernel<0>);
+// CUs get the instantiations with the grid size fixed at compile time; `loop`
+// selects the decode loop's instantiation.
+const void* decode_kernel_for(int grid, bool loop = false) {
+  if (loop)
+    return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256, true>)
+                       : reinterpret_cast<const void*>(mk_decode_kernel<0, true>);
+  return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256, false>)
+                     : reinterpret_cast<const void*>(mk_decode_kernel<0, false>);
 }
 
 int device_info(int dev, DeviceInfo* out) {
@@ -950,8 +964,11 @@ int device_info(int dev, DeviceInfo* out) {
       return fail(MK_ERR_HIP, "hipDeviceGetAttribute failed on device %d", dev);
     d.grid = cus;
     d.cus = cus;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel_for(cus), NT, 0) != hipSuccess)
+    int nbl = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel_for(cus), NT, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nbl, decode_kernel_for(cus, true), NT, 0) != hipSuccess)
       return fail(MK_ERR_HIP, "occupancy query failed");
+    nb = nb < nbl ? nb : nbl;
     d.ticks_per_s = (unsigned long long)(clk_khz > 0 ? clk_khz : 100000) * 1000ull;
     d.status = MK_OK;
     if (!coop) d.status = fail(MK_ERR_DEVICE, "device %d lacks cooperative launch", dev);
@@ -1176,7 +1193,7 @@ int launch_decode(const mk_weights* w, const mk_step_args* a, const DeviceInfo& 
   // kernel is bounded, so a workgroup that is never scheduled shows up as
   // MK_DEVERR_SYNC, not as a hang.
   const hipStream_t st = static_cast<hipStream_t>(a->stream);
-  const void* fn = decode_kernel_for(di.grid);
+  const void* fn = decode_kernel_for(di.grid, n_steps > 1 || tokens_out || step_clock);
   const hipError_t e = (a->flags & MK_FLAG_COOPERATIVE)
                            ? hipLaunchCooperativeKernel(fn, dim3(di.grid), dim3(NT), args, 0, st)
                            : hipLaunchKernel(fn, dim3(di.grid), dim3(NT), args, 0, st);
