@@ -9,7 +9,8 @@ position equal those of 24 single launches bit for bit. A loop followed by
 single steps continues the exchange-set and argmax-key state (equal to the
 same number of single steps). The step clock is monotonic. ``model.generate``
 (greedy, batch 1) runs the loop and returns the step-by-step tokens; a HIP graph
-of a loop replays it exactly. Refusals: batch > 1
+of a loop replays it exactly; the loop on generic grids and at KV positions near
+4000 equals single steps. Refusals: batch > 1
 workspace, hidden input, and positions past the cache (a device error, nothing
 written).
 """
@@ -207,3 +208,53 @@ def test_one_step_loop(model):
     assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
     c = clock.cpu()
     assert int(c[1]) > int(c[0]) > 0, c.tolist()
+
+
+@pytest.mark.parametrize("grid", [200, 128])
+def test_loop_on_a_generic_grid(model, grid):
+    """The loop's generic-grid instantiation (``mk_set_grid_size``): on 200 and
+    128 workgroups, 6 steps in one launch equal 6 single launches on the same
+    grid bit for bit (the step barrier's sub-counter shares follow the grid)."""
+    import mk_lib
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(48, seed=59))
+    st = snapshot(m)
+    mk_lib.set_grid_size(grid)
+    try:
+        assert mk_lib.grid_size() == grid
+        ref = singles(m, 6)
+        ref_kv = m.kv.clone()
+        restore(m, st)
+        got = loop(m, 6)
+    finally:
+        torch.cuda.synchronize()
+        mk_lib.set_grid_size(0)
+    say(f"[loop] grid {grid}: {got.tolist()}")
+    assert torch.equal(got, ref)
+    assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
+
+
+def test_loop_at_long_context():
+    """At KV positions near 4000 of a 4096-row cache (attention items of several
+    128-row groups, 8 splits per kv head), 10 steps in one launch equal 10
+    single launches bit for bit."""
+    need_gpu()
+    from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
+    from mk_weights import random_token_ids
+    S4 = 4096
+    m = NeuronLlamaForCausalLM("random:0", LlamaInferenceConfig(NeuronConfigLlamaMK(seq_len=S4)))
+    m.compile()
+    m.load()
+    m.prefill(random_token_ids(64, seed=61))
+    g = torch.Generator(device="cuda").manual_seed(3)
+    m.kv[:, :, :, :, 64:].normal_(generator=g)    # rows past the prompt: N(0,1) K/V up to the start position
+    m.pos.fill_(3990)
+    st = snapshot(m)
+    ref = singles(m, 10)
+    ref_kv = m.kv.clone()
+    restore(m, st)
+    got = loop(m, 10)
+    assert torch.equal(got, ref)
+    assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
+    assert int(m.pos.item()) == 4000
