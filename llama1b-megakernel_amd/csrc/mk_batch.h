@@ -93,6 +93,10 @@ struct BatchLayout {
   }
 };
 
+// The two-token-tile kernel (batches 17..32) for a grid of `grid` workgroups
+// (mk_batch_tile2.hip).
+const void* batch_kernel_tile2(int grid);
+
 // Grid check of the batched kernel on a device (occupancy 1 per CU); MK_OK or an MK_ERR code.
 int batch_device_check(int dev, char* msg, size_t msg_len);
 

@@ -46,6 +46,15 @@
 
 #include "mk.h"
 #include "mk_batch.h"
+// The two-token-tile instantiations (batches 17..32) are compiled in a
+// translation unit of their own, mk_batch_tile2.hip, which includes this file
+// with MK_BATCH_TILE2 defined. There the thread index is opaque to the
+// optimiser (tid() in mk_common.h): with less state kept live in registers
+// that kernel ran 1% faster at batch 32; the one-tile kernel, compiled here
+// with the plain index, ran 1.7% slower with it at batch 8.
+#ifdef MK_BATCH_TILE2
+#define MK_OPAQUE_TID 1
+#endif
 #include "mk_common.h"
 
 // Tuning constants (values measured best on MI355X; the alternatives and their
@@ -216,7 +225,7 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 __device__ __forceinline__ void arrive(uint32_t* ho, int sub) {
   wait_mem();
   lds_sync();
-  if (threadIdx.x == 0)
+  if (tid() == 0)
     __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ho) + (size_t)sub * CNT_LINE), 1u,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -440,8 +449,8 @@ __device__ __forceinline__ void stage_norm(const BCtx& c, rsrc_t src, bool gathe
 template <int MT, int TPR, bool GAMMA>
 __device__ __forceinline__ void norm_rows(const BCtx& c, const uint16_t* gamma, int r0, int r1, BLds<MT>& L) {
   constexpr int NCH = (H / 8) / TPR;
-  const int q = threadIdx.x & (TPR - 1);
-  for (int m = threadIdx.x / TPR; m < c.B; m += NT / TPR) {
+  const int q = tid() & (TPR - 1);
+  for (int m = tid() / TPR; m < c.B; m += NT / TPR) {
     uint16_t* row = &L.xn[m][0];
     for (int col = r0 + q; col < r1; col += TPR) L.res[m][col - r0] = row[col];
     u32x4 x[NCH], gvs[GAMMA ? NCH : 1];
@@ -503,7 +512,7 @@ __device__ __forceinline__ void stage_wait_raw(const BCtx& c, int r0, int r1, BL
   wait_vm_after<AFTER>();
   lds_sync();
   const int w = r1 - r0;
-  for (int i = threadIdx.x; i < c.B * w; i += NT) L.res[i / w][i % w] = L.xn[i / w][r0 + i % w];
+  for (int i = tid(); i < c.B * w; i += NT) L.res[i / w][i % w] = L.xn[i / w][r0 + i % w];
 }
 // The A operands of the QKV split-K MFMA (wave w: the K quarter [512w, 512w+512)
 // of every row, in mma_lds's lane layout: a[mt*KS + s]) read from the raw
@@ -664,7 +673,7 @@ __device__ __forceinline__ void tile_out(const f32x4 (&acc)[MT], BLds<MT>& L, F&
 template <int MT>
 __device__ __forceinline__ void plan_and_rope(BCtx& c, BLds<MT>& L) {
   const BParams& p = *c.p;
-  const int t = threadIdx.x;
+  const int t = tid();
   constexpr int RPT = (16 * MT * HD + NT - 1) / NT;   // RoPE words per thread at most
   uint32_t rv[RPT];
 #pragma unroll
@@ -823,7 +832,7 @@ __device__ __forceinline__ void phase_qkv(BCtx& c, int li, BLds<MT>& L, u32x4 (&
 template <int MT>
 __device__ __forceinline__ void phase_attn(BCtx& c, int li, BLds<MT>& L) {
   const BParams& p = *c.p;
-  const int lane = lane_id(), t = threadIdx.x;
+  const int lane = lane_id(), t = tid();
   const int nitems = L.cum[c.B];
   const rsrc_t rq = make_rsrc(c.sx(li, p.lay.sq_qkv), (size_t)c.B * QKV_ROWS * 2);
   bool waited = false;
@@ -1234,7 +1243,7 @@ __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
 template <int MT>
 __device__ __forceinline__ void phase_down2d(BCtx& c, int li, BLds<MT>& L) {
   const BParams& p = *c.p;
-  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id(), t = threadIdx.x;
+  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id(), t = tid();
   const bool last = li == p.n_layers - 1;
   const int n = c.w / DN_KQ, kq = c.w % DN_KQ;
   const int R0 = n * c.drpg, R1 = R0 + c.drpg, ntile = c.drpg / 16;
@@ -1335,7 +1344,7 @@ __device__ __forceinline__ void refill_sentinel_set(const BCtx& c, uint32_t epoc
   int lo, hi;
   share((int)(p.lay.sset / 16), c.G, c.w, lo, hi);
   const u32x4 ones = {~0u, ~0u, ~0u, ~0u};
-  for (int i = lo + (int)threadIdx.x; i < hi; i += NT)
+  for (int i = lo + (int)tid(); i < hi; i += NT)
     __builtin_amdgcn_raw_buffer_store_b128(ones, r, (int)((uint32_t)i * 16u), 0, AUX_SC1);
 }
 
@@ -1346,7 +1355,7 @@ __device__ __forceinline__ void prepare_next_launch(const BCtx& c, uint32_t epoc
   refill_sentinel_set(c, epoch);
   int lo, hi;
   share(c.cnt_words, c.G, c.w, lo, hi);
-  for (int i = lo + (int)threadIdx.x; i < hi; i += NT)
+  for (int i = lo + (int)tid(); i < hi; i += NT)
     __hip_atomic_store(c.cnt_other + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1462,7 +1471,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
       if (lgc) return;
       lds_sync();
       {   // thread t: token t / 8, rows 8*(t % 8) .. +7 of the round
-        const int t = threadIdx.x, m = t >> 3, r8 = (t & 7) * 8;
+        const int t = tid(), m = t >> 3, r8 = (t & 7) * 8;
         const int row0 = V0 + 16 * NWAVE * (u / UPT) + r8;   // (V0, V1 and rows multiples of 8)
         const bool ok = m < c.B && row0 < V1;
         const uint32_t off = ok ? ((uint32_t)m * (uint32_t)VOCAB + (uint32_t)row0) * 4u : OOB;
@@ -1492,7 +1501,7 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
       if ((lane & 15) == 0) L.key[wave][mt * 16 + (lane >> 4) * 4 + i] = k;
     }
   __syncthreads();
-  const int t = threadIdx.x;
+  const int t = tid();
   if (t < c.B) {
     unsigned long long k = L.key[0][t];
 #pragma unroll
@@ -1529,7 +1538,7 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   c.w = blockIdx.x;
   c.B = p.batch;
   c.prefill = (p.flags & MK_FLAG_PREFILL) != 0;
-  const int t = threadIdx.x;
+  const int t = tid();
   const uint32_t epoch = __hip_atomic_load(ctrl + C_EPOCH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int tok = 0, ps = 0;
   if (t < c.B) {
@@ -1630,6 +1639,21 @@ __global__ void __launch_bounds__(NT, 1) mk_batch_kernel(BParams p) {
   }
 }
 
+}  // namespace
+
+#ifdef MK_BATCH_TILE2
+
+namespace mk {
+// The two-tile kernel of this translation unit for a grid of `grid` workgroups.
+const void* batch_kernel_tile2(int grid) {
+  return grid == 256 ? reinterpret_cast<const void*>(mk_batch_kernel<2, 256>)
+                     : reinterpret_cast<const void*>(mk_batch_kernel<2, 0>);
+}
+}  // namespace mk
+
+#else
+
+namespace {
 struct BDev {
   int ready;
   int status;
@@ -1637,20 +1661,17 @@ struct BDev {
 };
 BDev g_bdev[64];
 std::mutex g_bdev_mu;
-
 }  // namespace
 
 namespace mk {
 
 // The batched kernel for `batch` tokens on a grid of `grid` workgroups: one
-// 16-row MFMA tile up to 16 tokens, two above; MI355X's 256 CUs get the
-// instantiations with the grid size fixed at compile time.
+// 16-row MFMA tile up to 16 tokens, two above (mk_batch_tile2.hip); MI355X's
+// 256 CUs get the instantiations with the grid size fixed at compile time.
 const void* batch_kernel_for(int batch, int grid) {
-  if (grid == 256)
-    return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 256>)
-                       : reinterpret_cast<const void*>(mk_batch_kernel<2, 256>);
-  return batch <= 16 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 0>)
-                     : reinterpret_cast<const void*>(mk_batch_kernel<2, 0>);
+  if (batch > 16) return batch_kernel_tile2(grid);
+  return grid == 256 ? reinterpret_cast<const void*>(mk_batch_kernel<1, 256>)
+                     : reinterpret_cast<const void*>(mk_batch_kernel<1, 0>);
 }
 
 int batch_device_check(int dev, char* msg, size_t msg_len) {
@@ -1734,3 +1755,5 @@ hipError_t batch_launch(const mk_weights* w, const mk_step_args* a, uint8_t* xch
 }
 
 }  // namespace mk
+
+#endif  // MK_BATCH_TILE2

@@ -33,6 +33,24 @@ constexpr uint32_t OOB = 0x80000000u;      // buffer offset past every resource
 constexpr float EPS = 1e-5f;
 constexpr float SM_SCALE = 0.125f;         // 1/sqrt(64)
 
+// The thread's index in its workgroup. A translation unit that defines
+// MK_OPAQUE_TID before including this header reads it through an empty
+// volatile asm at every use, so the compiler can neither hoist arithmetic on
+// it out of a loop nor merge two uses: values such as per-lane offsets and LDS
+// addresses are then recomputed where they are used instead of being kept in
+// registers across the loop. (The batched kernel's decode loop wraps a whole
+// step, 16 layers and the lm_head, in one loop; hoisted out of it, such
+// values stayed live through every layer and spilled.)
+__device__ __forceinline__ unsigned tid() {
+#ifdef MK_OPAQUE_TID
+  unsigned v = __builtin_amdgcn_workitem_id_x();
+  asm volatile("" : "+v"(v));
+  return v;
+#else
+  return threadIdx.x;
+#endif
+}
+
 constexpr size_t QKV_LAYER_BYTES = (size_t)QKV_ROWS * H * 2;
 constexpr size_t O_LAYER_BYTES = (size_t)H * H * 2;
 constexpr size_t GU_LAYER_BYTES = (size_t)2 * INTER * H * 2;
@@ -185,7 +203,7 @@ __device__ __forceinline__ Pair swap16(float a, float b) {
 }
 template <int N>
 __device__ __forceinline__ float reduce_rows(const float (&in)[N]) {
-  const int lane = threadIdx.x & 63;
+  const int lane = tid() & 63;
   float v[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) v[k] = in[k];
@@ -247,7 +265,7 @@ __device__ __forceinline__ float reduce_rows(const float (&in)[N]) {
 template <int N, bool MAX>
 __device__ __forceinline__ void reduce_stride8(float (&v)[N]) {
   static_assert(N == 4 || N == 32, "4 or 32 values");
-  const int lane = threadIdx.x & 63;
+  const int lane = tid() & 63;
   auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
 #pragma unroll
   for (int k = 0; k < N / 2; ++k) {
@@ -325,8 +343,8 @@ __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0x0f70);
 // after wait_mem().
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+__device__ __forceinline__ int lane_id() { return tid() & 63; }
+__device__ __forceinline__ int wave_id() { return tid() >> 6; }
 
 // Contiguous share [lo, hi) of `total` items for part `i` of `n`.
 // (32-bit division when the products fit: much shorter than the 64-bit one.)
@@ -357,7 +375,7 @@ struct Sync {
 };
 
 __device__ __forceinline__ void trace_mark(const Sync& s, int slot) {
-  if (s.trace && threadIdx.x == 0 && slot < MK_TRACE_SLOTS) s.trace[slot] = wall_clock64();
+  if (s.trace && tid() == 0 && slot < MK_TRACE_SLOTS) s.trace[slot] = wall_clock64();
 }
 // Slot MK_TRACE_DONE0 + 5*li + j: phase j (0 QKV, 1 ATTN, 2 O, 3 GU, 4 DOWN) of
 // run-layer li has issued its result stores.
@@ -366,7 +384,7 @@ __device__ __forceinline__ void trace_done(const Sync& s, int li, int j) {
 }
 // A diagnostic value (not a time) in one of the slots MK_TRACE_SLOTS-8 .. -2.
 __device__ __forceinline__ void trace_value(const Sync& s, int k, unsigned long long v) {
-  if (s.trace && threadIdx.x == 0 && k >= 0 && k < 7) s.trace[MK_TRACE_SLOTS - 8 + k] = v;
+  if (s.trace && tid() == 0 && k >= 0 && k < 7) s.trace[MK_TRACE_SLOTS - 8 + k] = v;
 }
 
 // True when a wait must give up: its time limit passed (the error bit is set
@@ -548,7 +566,7 @@ struct AttnRows {
   __device__ __forceinline__ int ngroups() const { return jc > j0 ? (jc - j0 + 32 * R - 1) / (32 * R) : 0; }
   template <int R>
   __device__ __forceinline__ void load(int gi, AttnGroupT<R>& g) const {
-    const int rl = threadIdx.x >> 3, ch = threadIdx.x & 7;
+    const int rl = tid() >> 3, ch = tid() & 7;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int j = j0 + gi * 32 * R + 32 * r + rl;
@@ -573,7 +591,7 @@ struct AttnRows {
 template <int R = ATT_R>
 __device__ __forceinline__ void attn_item(const AttnRows& rows, AttnGroupT<R>& first, const uint16_t* q_lds,
                                           bool fresh, float* part, AttnShared& sh) {
-  const int t = threadIdx.x, rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
+  const int t = tid(), rl = t >> 3, ch = t & 7, wave = wave_id(), lane = lane_id();
   u32x4 q[GQA];
 #pragma unroll
   for (int g = 0; g < GQA; ++g) q[g] = *reinterpret_cast<const u32x4*>(q_lds + g * HD + ch * 8);
@@ -791,7 +809,7 @@ template <int DEPTH = 1>
 __device__ __forceinline__ void attn_item_mx(const AttnRows& rows, AttnGroupMx (&ring)[DEPTH + 1],
                                              const uint16_t* q_lds, bool fresh, float* part, AttnShared& sh,
                                              uint16_t* att = nullptr, int tok = 0, int col0 = 0) {
-  const int t = threadIdx.x, wave = wave_id(), lane = lane_id(), n = lane & 15, q4 = lane >> 4;
+  const int t = tid(), wave = wave_id(), lane = lane_id(), n = lane & 15, q4 = lane >> 4;
   // B operands: q of head n (zero for the padding columns), times 1/8
   u32x4 qb[2];
 #pragma unroll
@@ -987,7 +1005,7 @@ constexpr int ATT_MERGE_MAX = 8;   // splits the polled merge reads at most
 template <bool POLL = true, int MAXS = ATT_MERGE_MAX, bool TILED = false>
 __device__ __forceinline__ void attn_merge_head(const Sync& sy, const float* part_head, int nsplit, uint16_t* att,
                                                 int tok = 0, int col0 = 0) {
-  const int t = threadIdx.x, g = t >> 6, d = t & 63;
+  const int t = tid(), g = t >> 6, d = t & 63;
   const rsrc_t r = make_rsrc(part_head, (size_t)nsplit * PART_FLOATS * 4);
   uint32_t m[MAXS], l[MAXS], o[MAXS];
   const unsigned long long t0 = wall_clock64();
