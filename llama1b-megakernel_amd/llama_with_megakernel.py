@@ -507,9 +507,13 @@ class NeuronLlamaForCausalLMMK:
                 raise ValueError(f"{n_steps} steps from position {p} exceed max_context_length {self.s_max}")
         out = tokens_out if tokens_out is not None else torch.empty(n_steps, dtype=torch.int32,
                                                                      device=self.pos.device)
-        mk_lib.decode_loop(self.weights, self.ws, self.k_caches, self.v_caches, self.pos, self.tokens, n_steps,
-                           tokens_out=out, step_clock=step_clock, logits=self.logits, next_token=self.tokens,
-                           hidden_out=self.hidden_out, flags=mk_lib.MK_FLAG_ADVANCE)
+        dec = self.launcher("decode")   # the same arguments, prebuilt
+        if torch.cuda.current_stream(self.pos.device).cuda_stream == dec.stream_ptr:
+            dec.loop(n_steps, tokens_out=out, step_clock=step_clock)
+        else:
+            mk_lib.decode_loop(self.weights, self.ws, self.k_caches, self.v_caches, self.pos, self.tokens, n_steps,
+                               tokens_out=out, step_clock=step_clock, logits=self.logits, next_token=self.tokens,
+                               hidden_out=self.hidden_out, flags=mk_lib.MK_FLAG_ADVANCE)
         return out
 
     @torch.no_grad()

@@ -421,12 +421,24 @@ class StepLauncher:
                                _ptr(tokens), _ptr(hidden_in), _ptr(pos), _ptr(hidden_out), _ptr(logits),
                                _ptr(next_token), flags, ws.buf.data_ptr(), ws.nbytes, st, _ptr(trace))
         self.weights = weights
+        self.stream_ptr = st
         self._fn = load().mk_decode_step
+        self._loop_fn = load().mk_decode_loop
         self._wref = ctypes.byref(self.weights)
         self._aref = ctypes.byref(self.args)
 
     def launch(self) -> None:
         rc = self._fn(self._wref, self._aref)
+        if rc != MK_OK:
+            check(rc)
+
+    def loop(self, n_steps: int, tokens_out: Optional[torch.Tensor] = None,
+             step_clock: Optional[torch.Tensor] = None) -> None:
+        """``mk_decode_loop`` with the same arguments: ``n_steps`` greedy steps
+        in one launch (tokens_out: int32 [n_steps]; step_clock: int64
+        [n_steps + 1]). No argument is rebuilt, so the host adds only the call
+        itself to the launch."""
+        rc = self._loop_fn(self._wref, self._aref, int(n_steps), _ptr(tokens_out), _ptr(step_clock))
         if rc != MK_OK:
             check(rc)
 

@@ -10,7 +10,8 @@ single steps continues the exchange-set and argmax-key state (equal to the
 same number of single steps). The step clock is monotonic. ``model.generate``
 (greedy, batch 1) runs the loop and returns the step-by-step tokens; a HIP graph
 of a loop replays it exactly; the loop on generic grids and at KV positions near
-4000 equals single steps. Refusals: batch > 1
+4000 equals single steps; ``model.decode_loop`` gives the same result on the
+stream of its prebuilt arguments and on a side stream. Refusals: batch > 1
 workspace, hidden input, and positions past the cache (a device error, nothing
 written).
 """
@@ -258,3 +259,25 @@ def test_loop_at_long_context():
     assert torch.equal(got, ref)
     assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
     assert int(m.pos.item()) == 4000
+
+
+def test_model_loop_on_a_side_stream(model):
+    """``model.decode_loop`` calls the prebuilt decode launcher's loop on the
+    stream that launcher was built for, and ``mk_decode_loop`` with fresh
+    arguments on any other current stream: same tokens and caches either way."""
+    from mk_weights import random_token_ids
+    m = model
+    m.prefill(random_token_ids(36, seed=61))
+    st = snapshot(m)
+    ref = m.decode_loop(5).cpu()
+    ref_kv = m.kv.clone()
+    restore(m, st)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        got = m.decode_loop(5)
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert m.ws.read_device_error() == 0
+    assert torch.equal(got.cpu(), ref)
+    assert torch.equal(m.kv.view(torch.int16), ref_kv.view(torch.int16))
