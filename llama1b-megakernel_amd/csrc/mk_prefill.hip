@@ -288,54 +288,51 @@ __global__ void __launch_bounds__(64) pf_reduce_norm(const float* part, const ui
   for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(xn + a_tile_off(t, i * 512 + lane * 8, H / 32)) = xs[i];
 }
 
-// The split-K tail of the QKV projection of short prompts (N = 3072), one
-// 64-thread workgroup per token row t: each RoPE pair p (columns 2p and
-// 2p + 1: dims d and d + 32 of a head) summed over the SPLITS fp32 partials
-// in split order and rounded to bf16, RoPE on the q and k pairs as the QKV
-// GEMM's epilogue does it, q to the q buffer, k and v to the caches at row
-// p0 + t.
+// The split-K tail of the QKV projection of short prompts (N = 3072): thread
+// (t, j) takes RoPE pairs 2j and 2j + 1 of token row t, i.e. columns 4j .. 4j + 3
+// (dims d, d + 32, d + 1, d + 33 of one head, d = 2j mod 32), in one 16-byte
+// load per split: each column summed over the SPLITS fp32 partials in split
+// order and rounded to bf16, RoPE on the q and k pairs as the QKV GEMM's
+// epilogue does it, q to the q buffer and k and v to the caches at row
+// p0 + t, two bf16 per 4-byte store. Grid (T, QKV_PAIRS / 2 / NT).
 template <int SPLITS>
-__global__ void __launch_bounds__(64) pf_qkv_finish(const float* part, const uint16_t* rope, uint16_t* q,
+__global__ void __launch_bounds__(NT) pf_qkv_finish(const float* part, const uint16_t* rope, uint16_t* q,
                                                     uint16_t* kc, uint16_t* vc, int T, int p0, int s_max) {
-  const int t = blockIdx.x, lane = lane_id();
-  if (t >= T) return;
-  const int pos = p0 + t;
-  const uint16_t* rrow = rope + (size_t)pos * (2 * HD);
-  constexpr int PER = 4;   // pairs per thread whose partials are loaded at once
-  static_assert(QKV_PAIRS % (64 * PER) == 0, "pair groups");
-#pragma unroll 1
-  for (int p0g = 0; p0g < QKV_PAIRS; p0g += 64 * PER) {
-    float2 pv[PER][SPLITS];
+  const int t = blockIdx.x, j = blockIdx.y * NT + (int)threadIdx.x;
+  if (t >= T || j >= QKV_PAIRS / 2) return;
+  const int pos = p0 + t, pr = 2 * j, hp = pr & 31;
+  float4 pv[SPLITS];
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
+  for (int sp = 0; sp < SPLITS; ++sp)
+    pv[sp] = *reinterpret_cast<const float4*>(part + ((size_t)sp * T + t) * QKV_ROWS + 4 * j);
+  float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
 #pragma unroll
-      for (int sp = 0; sp < SPLITS; ++sp)
-        pv[j][sp] = *reinterpret_cast<const float2*>(part + ((size_t)sp * T + t) * QKV_ROWS + 2 * (p0g + j * 64 + lane));
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int pr = p0g + j * 64 + lane, hp = pr & 31;
-      float va = 0.f, vb = 0.f;
-#pragma unroll
-      for (int sp = 0; sp < SPLITS; ++sp) {
-        va += pv[j][sp].x;
-        vb += pv[j][sp].y;
-      }
-      const float a = rbf(va), b = rbf(vb);   // (x[d], x[d + 32]) with d = hp
-      float o0 = a, o1 = b;
-      if (pr < Q_PAIRS + K_PAIRS) {
-        const float c0 = bf2f(rrow[hp]), s0 = bf2f(rrow[HD + hp]);
-        const float c1 = bf2f(rrow[hp + 32]), s1 = bf2f(rrow[HD + hp + 32]);
-        o0 = rbf(rbf(a * c0) + rbf(-b * s0));
-        o1 = rbf(rbf(b * c1) + rbf(a * s1));
-      }
-      uint16_t* dst;
-      if (pr < Q_PAIRS) dst = q + (size_t)t * H + (pr >> 5) * HD;
-      else if (pr < Q_PAIRS + K_PAIRS) dst = kc + ((size_t)((pr - Q_PAIRS) >> 5) * s_max + pos) * HD;
-      else dst = vc + ((size_t)((pr - Q_PAIRS - K_PAIRS) >> 5) * s_max + pos) * HD;
-      dst[hp] = (uint16_t)f2bf(o0);
-      dst[hp + 32] = (uint16_t)f2bf(o1);
-    }
+  for (int sp = 0; sp < SPLITS; ++sp) {
+    v0 += pv[sp].x;
+    v1 += pv[sp].y;
+    v2 += pv[sp].z;
+    v3 += pv[sp].w;
   }
+  // pair 2j: (x[d], x[d + 32]) = (a0, b0); pair 2j + 1: (x[d + 1], x[d + 33]) = (a1, b1)
+  const float a0 = rbf(v0), b0 = rbf(v1), a1 = rbf(v2), b1 = rbf(v3);
+  float o00 = a0, o01 = b0, o10 = a1, o11 = b1;
+  if (pr < Q_PAIRS + K_PAIRS) {
+    const uint16_t* rrow = rope + (size_t)pos * (2 * HD);
+    const uint32_t c0 = *reinterpret_cast<const uint32_t*>(rrow + hp);            // cos[d], cos[d + 1]
+    const uint32_t s0 = *reinterpret_cast<const uint32_t*>(rrow + HD + hp);       // sin[d], sin[d + 1]
+    const uint32_t c1 = *reinterpret_cast<const uint32_t*>(rrow + hp + 32);       // cos[d + 32], ...
+    const uint32_t s1 = *reinterpret_cast<const uint32_t*>(rrow + HD + hp + 32);  // sin[d + 32], ...
+    o00 = rbf(rbf(a0 * bf_lo(c0)) + rbf(-b0 * bf_lo(s0)));
+    o01 = rbf(rbf(b0 * bf_lo(c1)) + rbf(a0 * bf_lo(s1)));
+    o10 = rbf(rbf(a1 * bf_hi(c0)) + rbf(-b1 * bf_hi(s0)));
+    o11 = rbf(rbf(b1 * bf_hi(c1)) + rbf(a1 * bf_hi(s1)));
+  }
+  uint16_t* dst;
+  if (pr < Q_PAIRS) dst = q + (size_t)t * H + (pr >> 5) * HD;
+  else if (pr < Q_PAIRS + K_PAIRS) dst = kc + ((size_t)((pr - Q_PAIRS) >> 5) * s_max + pos) * HD;
+  else dst = vc + ((size_t)((pr - Q_PAIRS - K_PAIRS) >> 5) * s_max + pos) * HD;
+  *reinterpret_cast<uint32_t*>(dst + hp) = pack_bf2(o00, o10);
+  *reinterpret_cast<uint32_t*>(dst + hp + 32) = pack_bf2(o01, o11);
 }
 
 // xn (A-tile order [T16][2048]) = bf16(x * rsqrt(mean(x^2) + eps)) per token
@@ -621,9 +618,9 @@ hipError_t prefill_launch(const mk_weights* w, const mk_prefill_args* a, int cap
         hipLaunchKernelGGL(pf_gemm<EPI_PART>, dim3(mt * (QKV_ROWS / PF_TN), qs), dim3(NT), 0, st, g);
         const uint16_t* rope = static_cast<const uint16_t*>(w->rope);
         switch (qs) {   // qkv_splits gives 2, 4 or 8
-          case 2: hipLaunchKernelGGL(pf_qkv_finish<2>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
-          case 4: hipLaunchKernelGGL(pf_qkv_finish<4>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
-          default: hipLaunchKernelGGL(pf_qkv_finish<8>, dim3(T), dim3(64), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+          case 2: hipLaunchKernelGGL(pf_qkv_finish<2>, dim3(T, QKV_PAIRS / 2 / NT), dim3(NT), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+          case 4: hipLaunchKernelGGL(pf_qkv_finish<4>, dim3(T, QKV_PAIRS / 2 / NT), dim3(NT), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
+          default: hipLaunchKernelGGL(pf_qkv_finish<8>, dim3(T, QKV_PAIRS / 2 / NT), dim3(NT), 0, st, (const float*)part, rope, q, kc, vc, T, p0, a->s_max); break;
         }
         g.splits = 1;
       }
