@@ -245,15 +245,18 @@ def test_prefill_flag_needs_batched_workspace(setup):
 
 
 @pytest.mark.timeout(300)
-def test_layers_prefill_long_prompt_matches_chunks():
-    """A 1500-token prompt: the O and down projections of "layers" run unsplit
-    (12 row tiles of 128 tokens occupy the device) with the residual add in the
-    GEMM epilogue, where the short prompts above take the split-K path. Its
-    K/V rows agree with the "chunks" method's within the same relative bounds,
-    and so does the first decode step from each cache (per-step bounds)."""
+@pytest.mark.parametrize("n", [200, 383, 1500])
+def test_layers_prefill_matches_chunks(n):
+    """Prompts whose "layers" prefill takes each GEMM path: 200 tokens (the QKV
+    projection split over K in 4 parts, O and down in 8), 383 (QKV in 2, O and
+    down in 4), 1500 (12 row tiles of 128 tokens occupy the device: every
+    projection unsplit, the residual add in the GEMM epilogue). Their K/V rows
+    agree with the "chunks" method's within the same relative bounds as the
+    70-token prompt's against the oracle, and so does the first decode step
+    from each cache (per-step bounds)."""
     from llama_with_megakernel import LlamaInferenceConfig, NeuronConfigLlamaMK, NeuronLlamaForCausalLM
     from mk_weights import random_token_ids
-    S2, n = 2048, 1500
+    S2 = 2048
     cfg = LlamaInferenceConfig(NeuronConfigLlamaMK(seq_len=S2, max_context_length=S2))
     m = NeuronLlamaForCausalLM("random:0", cfg)
     m.compile()
@@ -275,6 +278,6 @@ def test_layers_prefill_long_prompt_matches_chunks():
         worst = max(worst, rel)
         assert rel <= KV_RMS_REL and d.max().item() <= KV_MAX_REL * kv_c[l].abs().max().item(), (l, rel)
     d = (lg_l - lg_c).abs()
-    say(f"[prefill] 1500 tokens, layers vs chunks: K/V worst rms rel {worst:.3e}; first step logits "
+    say(f"[prefill] {n} tokens, layers vs chunks: K/V worst rms rel {worst:.3e}; first step logits "
         f"max|d| {d.max():.3e} rms {d.pow(2).mean().sqrt():.3e}")
     assert d.max().item() <= STEP_MAX_TOL and d.pow(2).mean().sqrt().item() <= STEP_RMS_TOL
