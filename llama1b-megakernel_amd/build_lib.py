@@ -12,7 +12,8 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 REPO = HERE.parent
-SOURCES = [HERE / "csrc" / "mk_decode.hip", HERE / "csrc" / "mk_batch.hip", HERE / "csrc" / "mk_batch_tile2.hip",
+SOURCES = [HERE / "csrc" / "mk_decode.hip", HERE / "csrc" / "mk_decode_step.hip", HERE / "csrc" / "mk_batch.hip",
+           HERE / "csrc" / "mk_batch_tile2.hip",
            HERE / "csrc" / "mk_sample.hip", HERE / "csrc" / "mk_prefill.hip"]
 LIB = HERE / "libmk.so"
 

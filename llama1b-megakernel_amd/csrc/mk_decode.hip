@@ -67,6 +67,15 @@
 
 #include "mk.h"
 #include "mk_batch.h"
+// The single-step instantiations of the kernel are compiled in a translation
+// unit of their own, mk_decode_step.hip, which includes this file with
+// MK_DECODE_STEP_TU defined: there the thread index is opaque to the optimiser
+// (tid() in mk_common.h), which made one-layer launches 1.5% faster; the
+// decode loop's instantiation, compiled here with the plain index, ran 0.45%
+// slower with it.
+#ifdef MK_DECODE_STEP_TU
+#define MK_OPAQUE_TID 1
+#endif
 #include "mk_common.h"
 #include "mk_prefill.h"
 
@@ -411,7 +420,7 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, R
   uint16_t* xq = c.xb(li, X_QKV);
   uint16_t* const kcl = p.kc[li];
   uint16_t* const vcl = p.vc[li];
-  for (int lp = threadIdx.x; lp < P1 - P0; lp += NT) {
+  for (int lp = tid(); lp < P1 - P0; lp += NT) {
     const int pr = P0 + lp, d = pr & 31;
     const float a = rbf(L.val[2 * lp]), b = rbf(L.val[2 * lp + 1]);
     if (pr < Q_PAIRS) {
@@ -498,7 +507,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   c.s.timeout = p.timeout_ticks;
   c.s.trace = p.trace ? p.trace + (size_t)blockIdx.x * MK_TRACE_SLOTS : nullptr;
   trace_mark(c.s, 0);
-  if (LOOP && p.step_clock && blockIdx.x == 0 && threadIdx.x == 0) p.step_clock[0] = wall_clock64();
+  if (LOOP && p.step_clock && blockIdx.x == 0 && tid() == 0) p.step_clock[0] = wall_clock64();
   c.G = GFIX ? GFIX : (int)gridDim.x;
   c.w = blockIdx.x;
   // The control words, the position and the token first; then the first
@@ -521,12 +530,12 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     const size_t n = SET_BYTES / 16;
     int lo, hi;
     share((int)n, c.G, c.w, lo, hi);
-    for (int i = lo + threadIdx.x; i < hi; i += NT) other[i] = u32x4{~0u, ~0u, ~0u, ~0u};
+    for (int i = lo + tid(); i < hi; i += NT) other[i] = u32x4{~0u, ~0u, ~0u, ~0u};
   };
   const int pos0 = c.pos;   // a loop's step n runs at position pos0 + n
   const bool pos_ok = c.pos >= 0 && c.pos + n_steps <= p.s_max && c.pos + n_steps <= p.rope_rows;
   if (!p.do_lm || !pos_ok) refill(0);   // (the lm_head phase runs only with a valid position)
-  if (!pos_ok && blockIdx.x == 0 && threadIdx.x == 0)
+  if (!pos_ok && blockIdx.x == 0 && tid() == 0)
     __hip_atomic_fetch_or(c.s.err, MK_DEVERR_POS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   c.n_rows = c.pos + 1;
   if (p.hidden_in) {
@@ -557,7 +566,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     const unsigned long long key = __hip_atomic_load(key_ptr(n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     trace_mark(c.s, MK_TRACE_SLOTS - 2);
     int t = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
-    if (w == 0 && threadIdx.x == 0) {
+    if (w == 0 && tid() == 0) {
       if (p.tokens_out) p.tokens_out[n - 1] = t;
       if (p.step_clock) p.step_clock[n] = wall_clock64();
     }
@@ -574,7 +583,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     }
     // the step's RoPE row, read once; it goes to LDS with the first layer's input
     uint32_t rope_v = 0;
-    if (threadIdx.x < HD) rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[threadIdx.x];
+    if (tid() < HD) rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[tid()];
     {
       attn_split(c.n_rows, ATT_MAX_SPLIT, 32, c.nsplit, c.att_rows);
       int R0, R1;
@@ -610,7 +619,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         if (li == 0 && n > 0) step_entry(n, gidle);
       }
       phase_qkv(c, li, L, gidle, qs, [&]() {
-        if (li == 0 && threadIdx.x < HD) reinterpret_cast<uint32_t*>(L.rope)[threadIdx.x] = rope_v;
+        if (li == 0 && tid() < HD) reinterpret_cast<uint32_t*>(L.rope)[tid()] = rope_v;
       });
       if (li == 8) trace_value(c.s, 1, (unsigned long long)gpf.next);
       phase_attn(c, li, L);
@@ -813,7 +822,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       refill(n);
       // the next step's argmax key (read by every workgroup at the start of
       // this step, all of which have passed their first hand-overs by now)
-      if (!last_step && w == 0 && threadIdx.x == 0)
+      if (!last_step && w == 0 && tid() == 0)
         __hip_atomic_store(key_ptr(n + 1), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       u32x4 xs[4];
       lds_x2048(L.x, xs);
@@ -835,7 +844,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
         L.bidx[wave] = bidx;
       }
       __syncthreads();
-      if (threadIdx.x == 0) {
+      if (tid() == 0) {
         float b = L.best[0];
         int bi = L.bidx[0];
         for (int k = 1; k < NWAVE; ++k)
@@ -859,7 +868,7 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       wait_mem();
       __syncthreads();
       trace_mark(c.s, MK_TRACE_SLOTS - 4);   // the step's arrival
-      if (threadIdx.x == 0)
+      if (tid() == 0)
         __hip_atomic_fetch_add(p.step_cnt + (size_t)(w % STEP_LINES) * (STEP_LINE / 4), 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
       qkv_ring(c, 0, qs);
@@ -870,12 +879,12 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
   trace_mark(c.s, MK_TRACE_SLOTS - 1);
   wait_mem();
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid() == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(ctrl + C_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     L.last = prev == (uint32_t)(G - 1);
   }
   __syncthreads();
-  if (!L.last || threadIdx.x != 0) return;
+  if (!L.last || tid() != 0) return;
   ctrl[C_EXIT] = 0u;
   ctrl[C_EPOCH] = epoch + (pos_ok ? (uint32_t)n_steps : 1u);
   unsigned long long key = 0ull;
@@ -914,9 +923,29 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
 // Fill kernel: the first n_zero 16-byte units zeroed (the control block), the
 // rest set to the exchange sentinel (all ones).
 __global__ void mk_ws_init_kernel(u32x4* p, size_t n, size_t n_zero) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + tid(); i < n; i += (size_t)gridDim.x * blockDim.x)
     p[i] = i < n_zero ? u32x4{0u, 0u, 0u, 0u} : u32x4{~0u, ~0u, ~0u, ~0u};
 }
+
+}  // namespace
+
+#ifdef MK_DECODE_STEP_TU
+
+namespace mk {
+// The single-step kernel of this translation unit for a grid of `grid` workgroups.
+const void* decode_step_kernel(int grid) {
+  return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256, false>)
+                     : reinterpret_cast<const void*>(mk_decode_kernel<0, false>);
+}
+}  // namespace mk
+
+#else
+
+namespace mk {
+const void* decode_step_kernel(int grid);   // mk_decode_step.hip
+}  // namespace mk
+
+namespace {
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -948,8 +977,7 @@ const void* decode_kernel_for(int grid, bool loop = false) {
   if (loop)
     return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256, true>)
                        : reinterpret_cast<const void*>(mk_decode_kernel<0, true>);
-  return grid == 256 ? reinterpret_cast<const void*>(mk_decode_kernel<256, false>)
-                     : reinterpret_cast<const void*>(mk_decode_kernel<0, false>);
+  return decode_step_kernel(grid);
 }
 
 int device_info(int dev, DeviceInfo* out) {
@@ -1505,3 +1533,5 @@ int mk_layer_step(const mk_weights* w, int32_t layer, int32_t batch, int32_t s_m
 }
 
 }  // extern "C"
+
+#endif  // MK_DECODE_STEP_TU
