@@ -20,6 +20,8 @@ differs from the batch-1 kernel's, so results are compared with the oracle
   noise floor they sit on), next_token the argmax of the step's own logits,
   the same logits as the batch-1 kernel from the same state within those
   bounds, and the scatter position-exact over all 16 layers;
+* the same full step at batch 20 (the two-tile kernel with a partial second
+  tile): every sequence against the batch-1 kernel, two against the oracle;
 * bitwise repeatability, MK_FLAG_ADVANCE on every sequence, and a step with
   one position out of range refused as a whole (error bit, nothing written).
 """
@@ -316,3 +318,70 @@ def test_batched_step_bitwise_repeatable_and_advances(full16):
     assert torch.equal(outs[0][1], outs[1][1])
     assert torch.equal(outs[0][2].view(torch.int16), outs[1][2].view(torch.int16))
     assert torch.equal(outs[0][3].view(torch.int16), outs[1][3].view(torch.int16))
+
+
+def test_batched_step_two_tiles_partial(full16):
+    """A full 16-layer step at batch 20: the two-token-tile kernel (batches
+    17..32, its own translation unit) with a partial second tile (tokens 16..19;
+    rows 20..31 of the tile are MFMA padding). Each sequence's logits against the
+    batch-1 kernel's step from the same cache slice and, for two sequences,
+    against the oracle; next_token is each row's argmax, and only row pos of each
+    sequence's slice changes."""
+    import mk_lib
+    from mk_weights import random_token_ids
+    f = full16
+    lens = [3, 17, 40, 9, 25, 1, 60, 12, 33, 5, 48, 21, 2, 70, 14, 8, 29, 55, 6, 41]
+    B = len(lens)
+    w = f["w"]
+    kv = torch.zeros(16, 2, B, 8, S, 64, dtype=torch.bfloat16, device="cuda")
+    prompts = [random_token_ids(n, seed=900 + b) for b, n in enumerate(lens)]
+    pos1 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    tok1 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for b, ids in enumerate(prompts):   # prefill: the batch-1 kernel, one launch per prompt token
+        pos1.zero_()
+        l = mk_lib.StepLauncher(w, f["ws1"], [kv[i, 0, b:b + 1] for i in range(16)],
+                                [kv[i, 1, b:b + 1] for i in range(16)], pos1, tokens=tok1,
+                                flags=mk_lib.MK_FLAG_ADVANCE)
+        ids_dev = ids.to(device="cuda", dtype=torch.int32)
+        for i in range(len(ids) - 1):
+            tok1.copy_(ids_dev[i:i + 1])
+            l.launch()
+    torch.cuda.synchronize()
+    assert f["ws1"].read_device_error() == 0
+    kv_before = kv.clone()
+    ws = mk_lib.Workspace(B, S, torch.device("cuda"))
+    pos = torch.tensor([n - 1 for n in lens], dtype=torch.int32, device="cuda")
+    toks = torch.tensor([int(p[-1]) for p in prompts], dtype=torch.int32, device="cuda")
+    logits = torch.zeros(B, 128256, dtype=torch.float32, device="cuda")
+    nxt = torch.full((B,), -5, dtype=torch.int32, device="cuda")
+    mk_lib.decode_step(w, ws, [kv[i, 0] for i in range(16)], [kv[i, 1] for i in range(16)], pos, tokens=toks,
+                       logits=logits, next_token=nxt, batch=B)
+    torch.cuda.synchronize()
+    assert ws.read_device_error() == 0
+    kv_after = kv.clone()
+    logits, nxt = logits.cpu(), nxt.cpu()
+    worst = 0.0
+    for b, n in enumerate(lens):
+        p = n - 1
+        assert int(nxt[b]) == int(logits[b].argmax()), b
+        changed = (kv_after[:, :, b] != kv_before[:, :, b]).any(-1)   # [16, 2, 8, S]
+        assert changed.any(0).any(0).any(0).nonzero().flatten().tolist() == [p], b
+        kv[:, :, b].copy_(kv_before[:, :, b])
+        pos1.fill_(p)
+        tok1.fill_(int(prompts[b][-1]))
+        lg = torch.zeros(1, 128256, dtype=torch.float32, device="cuda")
+        mk_lib.decode_step(w, f["ws1"], [kv[i, 0, b:b + 1] for i in range(16)], [kv[i, 1, b:b + 1] for i in range(16)],
+                           pos1, tokens=tok1, logits=lg)
+        torch.cuda.synchronize()
+        d = (logits[b] - lg[0].cpu()).abs()
+        worst = max(worst, d.max().item())
+        assert d.max().item() <= STEP_MAX_TOL and d.pow(2).mean().sqrt().item() <= STEP_RMS_TOL, b
+    o = f["oracle"]
+    for b in (6, 19):   # one row of each token tile against the oracle
+        p = lens[b] - 1
+        cache = [(kv_before[l, 0, b].float().cpu(), kv_before[l, 1, b].float().cpu()) for l in range(16)]
+        ref, _ = o.forward(torch.tensor([int(prompts[b][-1])]), p, cache)
+        d = (logits[b] - ref[0]).abs()
+        say(f"[bstep] batch 20, seq {b} pos {p}: oracle max|d| {d.max():.3e} rms {d.pow(2).mean().sqrt():.3e}")
+        assert d.max().item() <= STEP_MAX_TOL and d.pow(2).mean().sqrt().item() <= STEP_RMS_TOL, b
+    say(f"[bstep] batch 20 (two tiles): worst max|d| against the batch-1 kernel {worst:.3e}")
