@@ -1104,7 +1104,10 @@ __device__ __forceinline__ void phase_gu(BCtx& c, int li, BLds<MT>& L, GuCopy& g
 template <int MT>
 __device__ __forceinline__ void phase_down(BCtx& c, int li, BLds<MT>& L) {
   const BParams& p = *c.p;
-  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  // (the thread index read opaquely in every translation unit, tid_opaque():
+  // the one-tile kernel measured 0.8% faster with it in the down projections)
+  const unsigned tix = tid_opaque();
+  const int l = p.first_layer + li, wave = (int)(tix >> 6), lane = (int)(tix & 63u);
   const bool last = li == p.n_layers - 1;
   int R0, R1;
   share(H, c.G, c.w, R0, R1);
@@ -1170,7 +1173,10 @@ template <int MT>
 __device__ __forceinline__ void phase_down_pair(BCtx& c, int li, BLds<MT>& L) {
   static_assert(MT == 1, "one token tile");
   const BParams& p = *c.p;
-  const int l = p.first_layer + li, wave = wave_id(), lane = lane_id();
+  // (the thread index read opaquely in every translation unit, tid_opaque():
+  // the one-tile kernel measured 0.8% faster with it in the down projections)
+  const unsigned tix = tid_opaque();
+  const int l = p.first_layer + li, wave = (int)(tix >> 6), lane = (int)(tix & 63u);
   const bool last = li == p.n_layers - 1;
   int R0, R1;
   share(H, c.G, c.w, R0, R1);

@@ -33,19 +33,22 @@ constexpr uint32_t OOB = 0x80000000u;      // buffer offset past every resource
 constexpr float EPS = 1e-5f;
 constexpr float SM_SCALE = 0.125f;         // 1/sqrt(64)
 
-// The thread's index in its workgroup. A translation unit that defines
-// MK_OPAQUE_TID before including this header reads it through an empty
-// volatile asm at every use, so the compiler can neither hoist arithmetic on
-// it out of a loop nor merge two uses: values such as per-lane offsets and LDS
+// The thread's index in its workgroup. tid_opaque() reads it through an
+// empty volatile asm, so the compiler can neither hoist arithmetic on it out
+// of a loop nor merge two reads: values such as per-lane offsets and LDS
 // addresses are then recomputed where they are used instead of being kept in
-// registers across the loop. (The batched kernel's decode loop wraps a whole
-// step, 16 layers and the lm_head, in one loop; hoisted out of it, such
-// values stayed live through every layer and spilled.)
-__device__ __forceinline__ unsigned tid() {
-#ifdef MK_OPAQUE_TID
+// registers across the layer loop. Whether that pays depends on the kernel
+// (it frees registers, and each read is a point the scheduler does not move
+// memory operations across): a translation unit that defines MK_OPAQUE_TID
+// before including this header gets it at every tid() use.
+__device__ __forceinline__ unsigned tid_opaque() {
   unsigned v = __builtin_amdgcn_workitem_id_x();
   asm volatile("" : "+v"(v));
   return v;
+}
+__device__ __forceinline__ unsigned tid() {
+#ifdef MK_OPAQUE_TID
+  return tid_opaque();
 #else
   return threadIdx.x;
 #endif
