@@ -179,6 +179,21 @@ struct BCtx {
   }
 };
 
+// The kernel's parameter block (its one explicit argument, at offset 0 of the
+// kernarg segment) and a uniform value, through opaque copies: the compiler
+// can neither hoist loads or arithmetic on them out of a loop nor merge them
+// with earlier ones (see tid() in mk_common.h).
+__device__ __forceinline__ const BParams* opaque_params() {
+  typedef const __attribute__((address_space(4))) BParams* KParamPtr;
+  KParamPtr k = (KParamPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(k));
+  return (const BParams*)k;
+}
+__device__ __forceinline__ int opaque_s(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
 __device__ __forceinline__ int xk(int li, int ph) { return 5 * li + ph; }
 
 // Integer reductions over the 64 lanes of a wave (every lane gets the result),
@@ -1526,21 +1541,6 @@ __device__ __forceinline__ void phase_lm(BCtx& c, BLds<MT>& L, uint32_t epoch) {
           (int)off, 0, 0);
     }
   }
-}
-
-// The kernel's parameter block (its one explicit argument, at offset 0 of the
-// kernarg segment) and a uniform value, through opaque copies: the compiler
-// can neither hoist loads or arithmetic on them out of a loop nor merge them
-// with earlier ones (see tid() in mk_common.h).
-__device__ __forceinline__ const BParams* opaque_params() {
-  typedef const __attribute__((address_space(4))) BParams* KParamPtr;
-  KParamPtr k = (KParamPtr)__builtin_amdgcn_kernarg_segment_ptr();
-  asm volatile("" : "+s"(k));
-  return (const BParams*)k;
-}
-__device__ __forceinline__ int opaque_s(int v) {
-  asm volatile("" : "+s"(v));
-  return v;
 }
 
 // GFIX: the grid size when known at compile time (the per-phase work splits
