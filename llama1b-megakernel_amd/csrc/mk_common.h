@@ -984,15 +984,6 @@ __device__ __forceinline__ void attn_item_mx(const AttnRows& rows, AttnGroupMx (
   lds_sync();   // LDS reuse by a following item
 }
 
-// Split of [0, n_rows) into nsplit items of `rows` rows (a multiple of 32):
-// one item per min_rows rows, at most max_split items.
-__device__ __forceinline__ void attn_split(int n_rows, int max_split, int min_rows, int& nsplit, int& rows) {
-  int ns = (n_rows + min_rows - 1) / min_rows;
-  ns = ns < max_split ? ns : max_split;
-  rows = ((n_rows + ns - 1) / ns + 31) / 32 * 32;
-  nsplit = (n_rows + rows - 1) / rows;
-}
-
 // Merge the nsplit partials of one kv head (split s at part_head + s * PART_FLOATS)
 // into the bf16 attention output of its 4 q heads:
 //   att = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s   (then cast to bf16)

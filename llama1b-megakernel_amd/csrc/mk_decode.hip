@@ -345,7 +345,7 @@ struct Ctx {
   // divisions by the grid size are not cheap on the GPU)
   int P0, P1;            // QKV RoPE pairs of the workgroup
   int qkv_n;             // QKV rows of this wave: 2*P0 + wave + 4*j, j < qkv_n
-  int nsplit, att_rows;  // attention: KV splits per kv head, rows per split
+  int nsplit;            // attention: KV splits per kv head
   Span o_rows;           // this wave's O rows (empty on workgroups with attention items)
   bool has_o;            // the workgroup has O rows
   Span gu_pairs;         // this wave's gate/up pairs
@@ -450,14 +450,21 @@ __device__ __forceinline__ void phase_qkv(Ctx& c, int li, Lds& L, Idle&& idle, R
   trace_done(c.s, li, 0);
 }
 
-// ATTN phase: the workgroup's attention items (kv head, KV split).
+// ATTN phase: the workgroup's attention items (kv head, KV split). The KV
+// rows form ng = ceil(n_rows / 32) groups of 32; split sp of a head takes the
+// groups [sp * ng / nsplit, (sp + 1) * ng / nsplit): one group per split below
+// 256 rows, else eight splits whose sizes differ by at most one group. (Eight
+// splits at every length from 256 rows on: with whole splits of a fixed size
+// the count drops to 6 or 7 over about half of the 384..1023 positions, and
+// those steps took 5-7 us longer.)
 __device__ __forceinline__ void phase_attn(Ctx& c, int li, Lds& L) {
-  const int nsplit = c.nsplit, rows = c.att_rows;
+  const int nsplit = c.nsplit;
   const int nitems = NKV * nsplit;
   const int lane = lane_id();
   for (int it = c.w; it < nitems; it += c.G) {
     const int h = it / nsplit, sp = it % nsplit;
-    const int j0 = sp * rows, j1 = min(j0 + rows, c.n_rows);
+    const int ng = (c.n_rows + 31) >> 5;
+    const int j0 = 32 * (sp * ng / nsplit), j1 = min(32 * ((sp + 1) * ng / nsplit), c.n_rows);
     const bool fresh = c.pos >= j0 && c.pos < j1;
     // the item's cached rows do not depend on this step: their first group is issued before the wait for q
     AttnRows ar;
@@ -585,7 +592,10 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
     uint32_t rope_v = 0;
     if (tid() < HD) rope_v = reinterpret_cast<const uint32_t*>(p.rope + (size_t)c.pos * (2 * HD))[tid()];
     {
-      attn_split(c.n_rows, ATT_MAX_SPLIT, 32, c.nsplit, c.att_rows);
+      {
+        const int ng = (c.n_rows + 31) >> 5;
+        c.nsplit = ng < ATT_MAX_SPLIT ? ng : ATT_MAX_SPLIT;
+      }
       int R0, R1;
       share(H, G, w, R0, R1);
       c.d_rows = wave_span(R0, R1);
