@@ -600,12 +600,19 @@ __global__ void __launch_bounds__(NT, 1) mk_decode_kernel(KParams p) {
       share(H, G, w, R0, R1);
       c.d_rows = wave_span(R0, R1);
       // O rows: the workgroups that run attention items (and merge the splits)
-      // get none, so h1 does not wait for the ones that finish attention last
+      // get none, so h1 does not wait for the ones that finish attention last.
+      // With eight splits per head, neither do the other workgroups below
+      // G - 128 (they start the gate/up prefetch instead): the last 128 take
+      // 16 rows each, O_RING per wave, one transposed reduction. (The 192
+      // workgroups from 64 on, 10-11 rows each: C3 steps 5 us longer; counts
+      // that put more than O_RING rows on a wave: 15-30 us longer.)
       int O0 = R0, O1 = R1;
       const int A = NKV * c.nsplit;   // workgroups [0, A) run attention items
       if (A <= G / 2) {
-        if (w < A) O0 = O1 = 0;
-        else share(H, G - A, w - A, O0, O1);
+        // workgroups [0, NO) have no O rows
+        const int NO = A == NKV * ATT_MAX_SPLIT ? max(A, G - H / (NWAVE * O_RING)) : A;
+        if (w < NO) O0 = O1 = 0;
+        else share(H, G - NO, w - NO, O0, O1);
       }
       c.o_rows = wave_span(O0, O1);
       c.has_o = O1 > O0;
