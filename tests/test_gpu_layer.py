@@ -1,7 +1,8 @@
 """GPU parity of one fused decoder layer (BASELINE config 2 shapes) against the oracle.
 
 Layer 0 of seed-0 synthetic weights, hidden ~ N(0,1), K/V cache [1,8,1024,64]
-bf16 ~ N(0,1), pos = 1023 (and a few other positions), run through
+bf16 ~ N(0,1), pos = 1023 and a few other positions (384 and 900: eight KV
+splits of unequal sizes, 1-2 and 3-4 groups of 32 rows), run through
 ``mk_layer_step`` / ``mk_decode_step`` in libmk.so and compared with
 ``OracleLlama`` in "mk" mode (same bf16 rounding points, fp32 accumulation):
 
@@ -60,7 +61,7 @@ def oracle_layer(sd, d, hidden_cpu, k0, v0, pos_val, mode="mk"):
     return h, cache
 
 
-@pytest.mark.parametrize("pos_val", [1023, 0, 63, 64, 500])
+@pytest.mark.parametrize("pos_val", [1023, 0, 63, 64, 500, 384, 900])
 def test_layer_matches_oracle(layer_setup, pos_val):
     sd, packed, d = layer_setup
     say(f"[layer] pos={pos_val}")

@@ -53,7 +53,7 @@ def run_layer(packed, hidden, kc, vc, pos_list, ws_batch):
 
 @pytest.mark.parametrize("pos_list,ws_batch", [
     ([4095], 1),                      # batch-1 kernel: 8 items of 512 rows (4 full groups each)
-    ([2000], 1),                      # batch-1 kernel: 256-row items, the last one partial
+    ([2000], 1),                      # batch-1 kernel: items of 224-256 rows (7-8 groups of 32)
     ([4095, 600, 2047, 3071], 4),     # batched kernel, ragged
     ([1500, 4095, 129, 3333, 2600, 4000, 700, 3900], 8),
 ])
