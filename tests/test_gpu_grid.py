@@ -4,7 +4,9 @@ workgroups than CUs, against the one-per-CU launch and the oracle.
 On MI355X the 256-workgroup grid runs kernels with the grid size fixed at
 compile time; every other grid (a device with another CU count, or a grid
 chosen with mk_set_grid_size) runs the generic variants, whose work splits
-divide by the runtime grid size. Here grids of 128 and 200 workgroups run:
+divide by the runtime grid size. Here grids of 128 and 200 workgroups run
+(and, for batch 1, 96 and 32: fewer workgroups than twice the 64 attention
+items, so every workgroup takes O rows; at 32 each runs two attention items):
 
 * the batch-1 step (16 layers, lm_head, argmax): with fewer workgroups a
   wave's GEMV rows outnumber its register ring, so the phases take the
@@ -98,7 +100,7 @@ def batch1_ref(setup):
     return got, ref, floor
 
 
-@pytest.mark.parametrize("grid", [0, 128, 200])
+@pytest.mark.parametrize("grid", [0, 128, 200, 96, 32])
 def test_batch1_generic_grid_matches_oracle(setup, batch1_ref, grid):
     from noise_variants import rms
     w, _ = setup
